@@ -1,0 +1,315 @@
+#!/usr/bin/env python3
+"""Benchmark of the MCKE kernel layer on one MI355X.
+
+One *step* runs every hot-path kernel once at its BASELINE.json shape, back to back
+on one stream (so each kernel starts with caches holding the previous kernel's
+data, not its own):
+
+  gemm      fp32 C = A B, M = N = K = 8192, MFMA variant        (the headline)
+  reduce    row sum and row max of X[8192 x 8192]
+  full_sum  sum of 2^26 values (kTwoPass with rows = 1)
+  softmax   row softmax of X[32768 x C], C in {128, 1024, 4096}
+  bias_gelu GELU_tanh(X + b) for X[16384 x 4096] and X[4096 x 1024]
+
+Inputs are generated on the host from seeds and are resident in HBM before the
+timed region.  W untimed steps, then exactly K timed steps bracketed by device
+synchronisation and HIP events; each launch is also bracketed by its own event
+pair on the same stream, which gives every kernel's average launch duration.
+
+Printed: one JSON line (rank 0, N = 1).  `value` is the GEMM's TFLOP/s; `ops` lists
+every kernel with its roofline fraction; `roofline` is the GEMM's; `cpu_baseline`
+times the CPU reference of the same GEMM on a bounded row slab.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from __graft_entry__ import load_package  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, AMD published
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix, AMD published
+
+METRIC = "fp32 GEMM TFLOP/s + reduce/softmax/bias-GELU HBM GB/s, % of roofline"
+
+
+def log(msg: str) -> None:
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+class Op:
+    """One kernel launch of the step, with its algorithmic work per launch."""
+
+    def __init__(self, name, launch, bound, work, unit, shape):
+        self.name, self.launch, self.bound = name, launch, bound
+        self.work, self.unit, self.shape = work, unit, shape   # bytes or flops per launch
+        self.times_ms: list[float] = []
+
+    def summary(self):
+        t = np.array(self.times_ms, dtype=np.float64)
+        avg = float(t.mean())
+        if self.bound == "mfma":
+            achieved = self.work / (avg * 1e-3) / 1e12
+            peak, unit = PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
+        else:
+            achieved = self.work / (avg * 1e-3) / 1e9
+            peak, unit = PEAK_HBM_GBS, "GB/s"
+        return {
+            "name": self.name, "shape": self.shape, "bound": self.bound,
+            "avg_ms": round(avg, 5), "median_ms": round(float(np.median(t)), 5),
+            "min_ms": round(float(t.min()), 5), "achieved": round(achieved, 2), "unit": unit,
+            "peak": peak, "frac": round(achieved / peak, 4),
+            "algorithmic_" + ("flops" if self.bound == "mfma" else "bytes"): self.work,
+        }
+
+
+def build_ops(m, stream):
+    D = m.DeviceBuffer
+    ops, keep = [], []
+    st = stream
+
+    def ck(status):
+        if not status.ok():
+            raise RuntimeError(str(status))
+
+    # --- GEMM 8192^3 (BASELINE configs[0] at its largest sweep size) ---------
+    n = 8192
+    log("generating GEMM inputs (2 x 8192^2 U[-1,1))")
+    a = D.from_array(m.fill_random(n * n, 0x6E33A))
+    b = D.from_array(m.fill_random(n * n, 0x8B10C))
+    c = D.zeros(n * n)
+    tile = m.gemm_mfma_default_tile(n, n, n)
+    keep += [a, b, c]
+    ops.append(Op("gemm_mfma_f32", lambda: ck(m.launch_gemm_f32(
+        a, b, c, n, n, n, 1.0, 0.0, m.GemmVariant.kMfmaF32, tile, st)),
+        "mfma", 2 * n * n * n, "flop", f"{n}x{n}x{n} tile {tile.astuple()}"))
+
+    # --- reductions --------------------------------------------
+    R = C_ = 8192
+    log("generating reduce input (8192^2 N(0,1))")
+    xr = D.from_array(m.fill_normal(R * C_, 0x5EED12345))
+    outr = D(R * 4)
+    keep += [xr, outr]
+    red_bytes = (R * C_ + R) * 4
+    for kind, nm in ((m.ReduceKind.kSum, "row_sum"), (m.ReduceKind.kMax, "row_max")):
+        ops.append(Op(nm, (lambda kind=kind: ck(m.launch_row_reduce_f32(
+            xr, outr, R, C_, kind, m.ReduceVariant.kWarpShuffle, st))),
+            "hbm", red_bytes, "byte", f"{R}x{C_}"))
+    N26 = 1 << 26
+    log("generating full-sum input (2^26 U[0,1))")
+    xs = D.from_array(m.fill_random(N26, 0xF011, 0.0, 1.0))
+    wsb = m.row_reduce_workspace_bytes(1, N26, m.ReduceVariant.kTwoPass)
+    ws, outs = D(wsb), D(4)
+    keep += [xs, ws, outs]
+    ops.append(Op("full_sum", lambda: ck(m.launch_row_reduce_f32(
+        xs, outs, 1, N26, m.ReduceKind.kSum, m.ReduceVariant.kTwoPass, ws, wsb, st)),
+        "hbm", (N26 + 1) * 4, "byte", "1x2^26"))
+
+    # --- softmax -----------------------------------------------
+    rows = 32768
+    for cols in (128, 1024, 4096):
+        log(f"generating softmax input (32768x{cols} N(0,4) + 1% spikes)")
+        x = m.fill_normal(rows * cols, 0x50F7A11 + cols, 0.0, 2.0)
+        rng = np.random.default_rng(cols)
+        spike_rows = rng.choice(rows, rows // 100, replace=False)
+        x[spike_rows * cols + rng.integers(0, cols, spike_rows.size)] += 30.0
+        dx, dy = D.from_array(x), D(rows * cols * 4)
+        keep += [dx, dy]
+        ops.append(Op(f"softmax_c{cols}", (lambda dx=dx, dy=dy, cols=cols: ck(
+            m.launch_row_softmax_f32(dx, dy, rows, cols, m.SoftmaxVariant.kOnlineOnePass, st))),
+            "hbm", 2 * rows * cols * 4, "byte", f"{rows}x{cols}"))
+
+    # --- bias + GELU(tanh) -------------------------------------
+    for (br, bc) in ((16384, 4096), (4096, 1024)):
+        log(f"generating bias+GELU input ({br}x{bc})")
+        dx = D.from_array(m.fill_normal(br * bc, 0xB1A5AC7 + br))
+        db = D.from_array(m.fill_random(bc, 0xB1A5B1A5, -0.5, 0.5))
+        dy = D(br * bc * 4)
+        keep += [dx, db, dy]
+        ops.append(Op(f"bias_gelu_{br}x{bc}", (lambda dx=dx, db=db, dy=dy, br=br, bc=bc: ck(
+            m.launch_bias_act_f32(dx, db, dy, br, bc, m.Activation.kGeluTanh, 4, st))),
+            "hbm", (2 * br * bc + bc) * 4, "byte", f"{br}x{bc}"))
+    m.device_synchronize()
+    return ops, keep, (a, b, c, n)
+
+
+def run_steps(m, stream, ops, steps, record):
+    """Enqueue `steps` steps back to back (no host synchronisation inside), each
+    launch bracketed by its own event pair when `record`."""
+    pairs = [[(m.Event(), m.Event()) for _ in ops] for _ in range(steps)] if record else None
+    t0, t1 = m.Event(), m.Event()
+    stream.synchronize()
+    t0.record(stream)
+    for s in range(steps):
+        for i, op in enumerate(ops):
+            if record:
+                pairs[s][i][0].record(stream)
+            op.launch()
+            if record:
+                pairs[s][i][1].record(stream)
+    t1.record(stream)
+    stream.synchronize()
+    if record:
+        for s in range(steps):
+            for i, op in enumerate(ops):
+                e0, e1 = pairs[s][i]
+                op.times_ms.append(e0.elapsed_ms(e1))
+    return t0.elapsed_ms(t1)
+
+
+def gemm_sweep(m, stream, iters=10):
+    """configs[0]'s sweep sizes, timed back to back (reported, not the headline)."""
+    D = m.DeviceBuffer
+    out = []
+    for n in (512, 1024, 2048, 4096):
+        a = D.from_array(m.fill_random(n * n, 0x6E33A))
+        b = D.from_array(m.fill_random(n * n, 0x8B10C))
+        c = D.zeros(n * n)
+        tile = m.gemm_mfma_default_tile(n, n, n)
+        for _ in range(3):
+            m.launch_gemm_f32(a, b, c, n, n, n, 1.0, 0.0, m.GemmVariant.kMfmaF32, tile,
+                              stream).throw_if_error()
+        e0, e1 = m.Event(), m.Event()
+        e0.record(stream)
+        for _ in range(iters):
+            m.launch_gemm_f32(a, b, c, n, n, n, 1.0, 0.0, m.GemmVariant.kMfmaF32, tile, stream)
+        e1.record(stream)
+        stream.synchronize()
+        ms = e0.elapsed_ms(e1) / iters
+        tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
+        out.append({"n": n, "tile": tile.astuple(), "avg_ms": round(ms, 5),
+                    "tflops": round(tf, 2), "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4)})
+        log(f"gemm sweep {n}^3: {ms:.4f} ms  {tf:.1f} TFLOP/s")
+    return out
+
+
+def cpu_baseline(m, gemm_bufs, seconds_target=12.0):
+    """The CPU reference GEMM (reference tests/reference.hpp:199-211: i-j-p loops,
+    double accumulation, one thread) on a row slab of the same 8192^3 problem,
+    and a parity check of the GPU's C on that slab.  Uses oracle/_ref (the
+    reference's own code) when it was built, else the plain-C restatement."""
+    import oracle
+
+    a, b, c, n = gemm_bufs
+    ha = a.download(n * n)
+    hb = b.download(n * n)
+    hc = c.download(n * n)
+    use_ref = oracle.ref_available()
+    kind = "reference" if use_ref else "port"
+    # Time one row first, then size the slab to ~seconds_target.
+    rows_done, elapsed = 0, 0.0
+    slab_rows = 1
+    want_rows = []
+    while elapsed < seconds_target and rows_done < n:
+        r0, r1 = rows_done, min(n, rows_done + slab_rows)
+        sa = ha[r0 * n:r1 * n]
+        out = np.zeros((r1 - r0) * n, np.float32)
+        t = time.perf_counter()
+        if use_ref:
+            got = oracle.Ref.gemm(sa, hb, out, r1 - r0, n, n, 1.0, 0.0)
+        else:
+            got = oracle.gemm(sa, hb, out, r1 - r0, n, n, 1.0, 0.0)
+        elapsed += time.perf_counter() - t
+        want_rows.append(got)
+        rows_done = r1
+        per_row = elapsed / rows_done
+        slab_rows = max(1, min(64, int((seconds_target - elapsed) / per_row)))
+    want = np.concatenate(want_rows)
+    got = hc[:rows_done * n]
+    r = oracle.compare(got, want, oracle.tol_gemm(n), oracle.abs_tol_gemm(n))
+    flops = 2.0 * rows_done * n * n
+    return {
+        "value": round(flops / elapsed / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+        "kind": kind,
+        "sample": f"rows 0..{rows_done - 1} of C for the 8192^3 GEMM ({rows_done}x8192x8192, "
+                  f"{elapsed:.1f} s, 1 thread of {os.cpu_count()} host cores, double "
+                  f"accumulation in the reference's i-j-p order)",
+        "parity_on_sample": {"ok": bool(r.ok), "max_abs_err": r.max_abs_err,
+                             "max_rel_err": r.max_rel_err,
+                             "tol": f"rel tol_gemm(8192)={oracle.tol_gemm(n):.3g} + abs "
+                                    f"abs_tol_gemm(8192)={oracle.abs_tol_gemm(n):.3g}"},
+    }
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-sweep", action="store_true", help="skip the GEMM size sweep")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = p.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "kernel layer has no multi-GPU path to measure.", file=sys.stderr)
+        return 2
+
+    m = load_package()
+    info = m.require_gpu()
+    log(f"device: {info.name.decode()} {info.arch.decode()} CUs={info.sm_count}")
+    stream = m.Stream()
+    ops, keep, gemm_bufs = build_ops(m, stream)
+
+    log(f"warmup: {args.warmup} steps")
+    run_steps(m, stream, ops, args.warmup, record=False)
+    log(f"timed: {args.steps} steps")
+    total_ms = run_steps(m, stream, ops, args.steps, record=True)
+    summaries = [op.summary() for op in ops]
+    for s in summaries:
+        log(f"{s['name']:>20s} {s['avg_ms']:.4f} ms  {s['achieved']:.1f} {s['unit']}  "
+            f"({100 * s['frac']:.1f}% of {s['peak']})")
+
+    sweep = [] if args.no_sweep else gemm_sweep(m, stream)
+    gemm = summaries[0]
+    cpu = None
+    if not args.no_cpu:
+        log(f"cpu baseline: reference GEMM on a row slab (~{args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline(m, gemm_bufs, args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']} TFLOP/s ({cpu['sample']})")
+
+    line = {
+        "metric": METRIC,
+        "value": gemm["achieved"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded fill_random U[-1,1) / Box-Muller N(mu,sigma^2) at "
+                "BASELINE.json shapes, resident in HBM",
+        "config": {
+            "workload": "fp32 GEMM 8192^3 (kMfmaF32) headline; step also runs row sum/max "
+                        "8192x8192, full sum 2^26, softmax 32768x{128,1024,4096}, "
+                        "bias+GELU_tanh 16384x4096 and 4096x1024",
+            "gemm_tile": list(m.gemm_mfma_default_tile(8192, 8192, 8192).astuple()),
+            "device": info.name.decode(),
+        },
+        "roofline": {
+            "bound": "mfma", "achieved": gemm["achieved"], "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s", "frac": gemm["frac"], "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "ops": summaries,
+        "gemm_sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+    del keep
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

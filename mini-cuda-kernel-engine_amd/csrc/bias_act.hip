@@ -1,0 +1,229 @@
+// bias_act.hip -- fused y = act(x + bias[col]) and the unfused baseline pair.
+//
+// Replaces kernels/bias_act.cu (launchers bias_act.cu:269-331, validation :208-229).
+// HBM-bound: 4 bytes in + 4 bytes out per element (+ the bias row once per
+// column strip).  The design for gfx950:
+//   * 256-thread workgroups (4 wave64s); thread t of column strip blockIdx.x owns
+//     VW consecutive columns, so a wave issues 64 x VW x 4 contiguous bytes
+//     (1 KiB at VW = 4: 16-byte global_load_dwordx4 per lane);
+//   * the bias vector for those columns is loaded once and kept in registers;
+//   * rows are walked with a stride of gridDim.y, four rows per iteration, so
+//     each lane has four independent 16-byte loads in flight before it computes;
+//   * x and y are streamed with non-temporal loads/stores.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "common.hpp"
+#include "device_math.hpp"
+
+namespace mcke_amd {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowUnroll = 4;
+
+template <int VW, int ACT>
+__global__ __launch_bounds__(kThreads) void bias_act_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ bias,
+                                                            float* __restrict__ y,
+                                                            int64_t rows, int64_t cols_v) {
+  using V = Vec<VW>;
+  const int64_t cv = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (cv >= cols_v) return;
+  const V bv = reinterpret_cast<const V*>(bias)[cv];
+  const V* __restrict__ xv = reinterpret_cast<const V*>(x) + cv;
+  V* __restrict__ yv = reinterpret_cast<V*>(y) + cv;
+  const int64_t stride = gridDim.y;
+  for (int64_t r = blockIdx.y; r < rows; r += kRowUnroll * stride) {
+    V a[kRowUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t rr = r + u * stride;
+      if (rr < rows) a[u] = ld_stream(xv + rr * cols_v);
+    }
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t rr = r + u * stride;
+      if (rr < rows) {
+        V o;
+        if constexpr (VW == 1) {
+          o = act_xb<ACT>(a[u], bv);
+        } else {
+#pragma unroll
+          for (int i = 0; i < VW; ++i) o[i] = act_xb<ACT>(a[u][i], bv[i]);
+        }
+        st_stream(yv + rr * cols_v, o);
+      }
+    }
+  }
+}
+
+// y = act(x) over a flat array (the unfused pair's second kernel).
+template <int VW, int ACT>
+__global__ __launch_bounds__(kThreads) void activation_kernel(const float* __restrict__ x,
+                                                              float* __restrict__ y,
+                                                              int64_t n_v) {
+  using V = Vec<VW>;
+  const V* __restrict__ xv = reinterpret_cast<const V*>(x);
+  V* __restrict__ yv = reinterpret_cast<V*>(y);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n_v;
+       i += stride) {
+    const V a = ld_stream(xv + i);
+    V o;
+    if constexpr (VW == 1) {
+      o = act_xb<ACT>(a, 0.0f);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) o[j] = act_xb<ACT>(a[j], 0.0f);
+    }
+    st_stream(yv + i, o);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void vector_add_kernel(const float* __restrict__ a,
+                                                              const float* __restrict__ b,
+                                                              float* __restrict__ out,
+                                                              size_t n) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
+    out[i] = a[i] + b[i];
+}
+
+int validate_2d(const char* who, const float* x, const float* y, int64_t rows, int64_t cols,
+                int vw) {
+  if (!x || !y) return invalid(std::string(who) + ": null pointer");
+  if (rows < 0 || cols < 0) return invalid(std::string(who) + ": negative extent");
+  if (vw != 1 && vw != 2 && vw != 4)
+    return invalid(std::string(who) + ": vector_width must be 1, 2 or 4, got " +
+                   std::to_string(vw));
+  if (cols % vw != 0)
+    return invalid(std::string(who) + ": cols (" + std::to_string(cols) +
+                   ") must be a multiple of vector_width (" + std::to_string(vw) +
+                   "); use max_vector_width_f32() to pick a legal width");
+  const std::size_t align = sizeof(float) * static_cast<std::size_t>(vw);
+  if (!aligned(x, align) || !aligned(y, align))
+    return invalid(std::string(who) + ": pointer not " + std::to_string(align) +
+                   "-byte aligned");
+  return ok();
+}
+
+// Row dimension of the grid: enough workgroups that every lane walks about
+// kRowUnroll rows per iteration with the whole chip busy, capped at the
+// hardware's 65535 and at the caller's max_row_blocks.
+dim3 grid_2d(int64_t rows, int64_t cols_v, int max_row_blocks) {
+  const int64_t gx = (cols_v + kThreads - 1) / kThreads;
+  int64_t gy = (rows + kRowUnroll - 1) / kRowUnroll;
+  if (gy > 65535) gy = 65535;
+  if (max_row_blocks > 0 && gy > max_row_blocks) gy = max_row_blocks;
+  if (gy < 1) gy = 1;
+  return dim3(static_cast<unsigned>(gx > 0 ? gx : 1), static_cast<unsigned>(gy), 1u);
+}
+
+template <int VW>
+int launch_fused_vw(const float* x, const float* bias, float* y, int64_t rows, int64_t cols,
+                    int act, hipStream_t s, int max_row_blocks) {
+  const int64_t cols_v = cols / VW;
+  const dim3 grid = grid_2d(rows, cols_v, max_row_blocks);
+  switch (act) {
+    case kActNone: bias_act_kernel<VW, kActNone><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v); break;
+    case kActRelu: bias_act_kernel<VW, kActRelu><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v); break;
+    case kActGeluErf: bias_act_kernel<VW, kActGeluErf><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v); break;
+    case kActGeluTanh: bias_act_kernel<VW, kActGeluTanh><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v); break;
+    default: return invalid("launch_bias_act_f32: unknown activation " + std::to_string(act));
+  }
+  MCKE_LAUNCH_CHECK("bias_act_kernel");
+  return ok();
+}
+
+template <int VW>
+int launch_act_vw(const float* x, float* y, int64_t n, int act, hipStream_t s) {
+  const int64_t n_v = n / VW;
+  int64_t blocks = (n_v + kThreads - 1) / kThreads;
+  if (blocks > 8192) blocks = 8192;
+  const unsigned g = static_cast<unsigned>(blocks);
+  switch (act) {
+    case kActNone: activation_kernel<VW, kActNone><<<g, kThreads, 0, s>>>(x, y, n_v); break;
+    case kActRelu: activation_kernel<VW, kActRelu><<<g, kThreads, 0, s>>>(x, y, n_v); break;
+    case kActGeluErf: activation_kernel<VW, kActGeluErf><<<g, kThreads, 0, s>>>(x, y, n_v); break;
+    case kActGeluTanh: activation_kernel<VW, kActGeluTanh><<<g, kThreads, 0, s>>>(x, y, n_v); break;
+    default: return invalid("launch_activation_f32: unknown activation " + std::to_string(act));
+  }
+  MCKE_LAUNCH_CHECK("activation_kernel");
+  return ok();
+}
+
+}  // namespace
+}  // namespace mcke_amd
+
+using namespace mcke_amd;
+
+extern "C" {
+
+int mcke_max_vector_width_f32(const void* p, int64_t cols) {
+  for (int w = 4; w > 1; w >>= 1)
+    if (cols % w == 0 && aligned(p, sizeof(float) * static_cast<std::size_t>(w))) return w;
+  return 1;
+}
+
+int mcke_launch_bias_act_f32(const float* x, const float* bias, float* y, int64_t rows,
+                             int64_t cols, int act, int vector_width, void* stream,
+                             int max_row_blocks) {
+  if (rows == 0 || cols == 0) return ok();   // an empty grid is a launch error
+  if (!bias) return invalid("launch_bias_act_f32: null bias");
+  if (int rc = validate_2d("launch_bias_act_f32", x, y, rows, cols, vector_width)) return rc;
+  if (!aligned(bias, sizeof(float) * static_cast<std::size_t>(vector_width)))
+    return invalid("launch_bias_act_f32: bias pointer not aligned");
+  if (x == y)
+    return invalid("launch_bias_act_f32: in-place (x == y) violates the __restrict__ contract");
+  if (act < 0 || act > 3)
+    return invalid("launch_bias_act_f32: unknown activation " + std::to_string(act));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (vector_width) {
+    case 1: return launch_fused_vw<1>(x, bias, y, rows, cols, act, s, max_row_blocks);
+    case 2: return launch_fused_vw<2>(x, bias, y, rows, cols, act, s, max_row_blocks);
+    default: return launch_fused_vw<4>(x, bias, y, rows, cols, act, s, max_row_blocks);
+  }
+}
+
+int mcke_launch_bias_add_f32(const float* x, const float* bias, float* y, int64_t rows,
+                             int64_t cols, int vector_width, void* stream) {
+  return mcke_launch_bias_act_f32(x, bias, y, rows, cols, kActNone, vector_width, stream, 0);
+}
+
+int mcke_launch_activation_f32(const float* x, float* y, int64_t n, int act, int vector_width,
+                               void* stream) {
+  if (n == 0) return ok();
+  if (!x || !y) return invalid("launch_activation_f32: null pointer");
+  if (n < 0) return invalid("launch_activation_f32: negative extent");
+  if (vector_width != 1 && vector_width != 2 && vector_width != 4)
+    return invalid("launch_activation_f32: vector_width must be 1, 2 or 4");
+  if (n % vector_width != 0)
+    return invalid("launch_activation_f32: n must be a multiple of vector_width");
+  const std::size_t align = sizeof(float) * static_cast<std::size_t>(vector_width);
+  if (!aligned(x, align) || !aligned(y, align))
+    return invalid("launch_activation_f32: pointer not aligned");
+  if (act < 0 || act > 3)
+    return invalid("launch_activation_f32: unknown activation " + std::to_string(act));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (vector_width) {
+    case 1: return launch_act_vw<1>(x, y, n, act, s);
+    case 2: return launch_act_vw<2>(x, y, n, act, s);
+    default: return launch_act_vw<4>(x, y, n, act, s);
+  }
+}
+
+int mcke_launch_vector_add_f32(const float* a, const float* b, float* out, size_t n,
+                               void* stream) {
+  if (n == 0) return ok();
+  if (!a || !b || !out) return invalid("launch_vector_add_f32: null pointer");
+  size_t blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 8192) blocks = 8192;
+  vector_add_kernel<<<static_cast<unsigned>(blocks), kThreads, 0,
+                      static_cast<hipStream_t>(stream)>>>(a, b, out, n);
+  MCKE_LAUNCH_CHECK("vector_add_kernel");
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,277 @@
+// gemm_mfma.hpp -- fp32 GEMM on the CDNA matrix cores (v_mfma_f32_32x32x2_f32).
+//
+// C[M,N] = alpha * A[M,K] B[K,N] + beta * C, row-major, fp32 in and out, fp32
+// accumulation.  This is the new appended GemmVariant (kMfmaF32); the reference's
+// ladder kernels (gemm.cu:125-588) have no counterpart because the reference has
+// no matrix-core path.
+//
+// Workgroup: 256 lanes = 4 wave64s in a 2 x 2 grid; the workgroup owns a BM x BN
+// tile of C, each wave a WM x WN sub-tile = (WM/32) x (WN/32) MFMA 32x32 tiles,
+// kept in accumulation registers for the whole K loop.
+//
+// K is staged BK at a time through an LDS double buffer:
+//   As[BM][BK + 4]   A row-major (k contiguous); the +4 pad puts the 8 rows read
+//                    by an 8-lane 16-byte group on 8 disjoint bank quads;
+//   Bs[BK][BN]       B row-major (n contiguous).
+// One barrier per K step: the next step's global loads are issued before the
+// MFMAs of the current step and written to the other buffer after them.
+//
+// Operand delivery.  v_mfma_f32_32x32x2_f32 takes one A and one B value per lane:
+// lane l supplies A[i = l%32][kslot = l/32] and B[kslot = l/32][j = l%32].  The
+// K order inside a step is free (a sum), so lane half h = l/32 walks the k range
+// [h*BK/2, (h+1)*BK/2): then a lane's next four A values are contiguous in As and
+// arrive in one 16-byte ds_read per m-tile.  For B the N order is permuted
+// instead: within a wave's WN columns, MFMA n-tile j at lane column c holds
+// actual column NT*c + j, so one 4*NT-byte ds_read per k delivers a lane's
+// values for all NT n-tiles -- and in the epilogue the same lane holds NT
+// adjacent columns of each output row, which become one 16-byte global store.
+//
+// Accumulator layout of one 32x32 tile (lane l, register r = 0..15):
+//   row = 8*(r/4) + 4*(l/32) + (r%4),   col = l%32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "device_math.hpp"
+
+namespace mcke_amd {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kMfmaThreads = 256;
+constexpr int kXcds = 8;       // gfx950: workgroups are dealt round-robin to 8 XCDs
+constexpr int kGroupM = 8;     // tile-row grouping for L2 reuse within an XCD
+
+template <int NT> struct BVec;
+template <> struct BVec<1> { using type = float; };
+template <> struct BVec<2> { using type = f32x2; };
+template <> struct BVec<4> { using type = f32x4; };
+
+// Workgroup id -> (tile_m, tile_n).  Consecutive workgroup ids land on different
+// XCDs (id % 8), so ids are first regrouped so that each XCD sees a contiguous
+// run of logical tiles, and logical tiles are then walked kGroupM tile-rows at a
+// time so concurrently running tiles share A row-slabs and B column-slabs in
+// that XCD's L2.
+__device__ __forceinline__ void mfma_tile_coords(int wg, int tiles_m, int tiles_n, int& tm,
+                                                 int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int full = total - (total % kXcds);
+  int t = wg;
+  if (wg < full) t = (wg % kXcds) * (full / kXcds) + wg / kXcds;
+  const int in_group = kGroupM * tiles_n;
+  const int g = t / in_group;
+  const int first_m = g * kGroupM;
+  const int gsz = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+  const int local = t % in_group;
+  tm = first_m + local % gsz;
+  tn = local / gsz;
+}
+
+template <int BM, int BN, int BK, bool VEC>
+struct MfmaStage {
+  static constexpr int kLdA = BK + 4;
+  static constexpr int kLdB = BN;
+  static constexpr int kAFloats = BM * kLdA;
+  static constexpr int kBFloats = BK * kLdB;
+  static constexpr int kStageFloats = kAFloats + kBFloats;
+  // Per-lane global loads per stage.
+  static constexpr int kAVec = BM * BK / 4 / kMfmaThreads;   // float4 loads of A
+  static constexpr int kBVec = BK * BN / 4 / kMfmaThreads;   // float4 loads of B
+  static constexpr int kAScl = BM * BK / kMfmaThreads;       // scalar loads of A
+  static constexpr int kBScl = BK * BN / kMfmaThreads;       // scalar loads of B
+  static_assert(BM * BK % (4 * kMfmaThreads) == 0 && BK * BN % (4 * kMfmaThreads) == 0,
+                "stage must divide evenly over the workgroup");
+
+  // Registers holding one stage between its global load and its LDS store.
+  struct Regs {
+    f32x4 a[VEC ? kAVec : 1];
+    f32x4 b[VEC ? kBVec : 1];
+    float as[VEC ? 1 : kAScl];
+    float bs[VEC ? 1 : kBScl];
+  };
+
+  // Loads K columns [k0, k0 + BK) of the block's A rows and B columns, zero-filling
+  // everything outside [0, M) x [0, K) and [0, K) x [0, N).
+  static __device__ __forceinline__ void load(Regs& R, const float* __restrict__ A,
+                                              const float* __restrict__ B, int M, int N,
+                                              int K, int m0, int n0, int k0) {
+    const int t = threadIdx.x;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < kAVec; ++i) {
+        const int li = i * kMfmaThreads + t;
+        const int row = li / (BK / 4), c4 = li % (BK / 4);
+        const int gm = m0 + row, gk = k0 + 4 * c4;
+        // K % 4 == 0 on this path, so a float4 is either fully in range or fully out.
+        if (gm < M && gk < K)
+          R.a[i] = *reinterpret_cast<const f32x4*>(A + static_cast<int64_t>(gm) * K + gk);
+        else
+          R.a[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int i = 0; i < kBVec; ++i) {
+        const int li = i * kMfmaThreads + t;
+        const int kr = li / (BN / 4), c4 = li % (BN / 4);
+        const int gk = k0 + kr, gn = n0 + 4 * c4;
+        if (gk < K && gn < N)
+          R.b[i] = *reinterpret_cast<const f32x4*>(B + static_cast<int64_t>(gk) * N + gn);
+        else
+          R.b[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kAScl; ++i) {
+        const int li = i * kMfmaThreads + t;
+        const int row = li / BK, col = li % BK;
+        const int gm = m0 + row, gk = k0 + col;
+        R.as[i] = (gm < M && gk < K) ? A[static_cast<int64_t>(gm) * K + gk] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < kBScl; ++i) {
+        const int li = i * kMfmaThreads + t;
+        const int kr = li / BN, col = li % BN;
+        const int gk = k0 + kr, gn = n0 + col;
+        R.bs[i] = (gk < K && gn < N) ? B[static_cast<int64_t>(gk) * N + gn] : 0.0f;
+      }
+    }
+  }
+
+  static __device__ __forceinline__ void store(const Regs& R, float* __restrict__ stage) {
+    float* As = stage;
+    float* Bs = stage + kAFloats;
+    const int t = threadIdx.x;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < kAVec; ++i) {
+        const int li = i * kMfmaThreads + t;
+        const int row = li / (BK / 4), c4 = li % (BK / 4);
+        *reinterpret_cast<f32x4*>(As + row * kLdA + 4 * c4) = R.a[i];
+      }
+#pragma unroll
+      for (int i = 0; i < kBVec; ++i) {
+        const int li = i * kMfmaThreads + t;
+        const int kr = li / (BN / 4), c4 = li % (BN / 4);
+        *reinterpret_cast<f32x4*>(Bs + kr * kLdB + 4 * c4) = R.b[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kAScl; ++i) {
+        const int li = i * kMfmaThreads + t;
+        As[(li / BK) * kLdA + li % BK] = R.as[i];
+      }
+#pragma unroll
+      for (int i = 0; i < kBScl; ++i) {
+        const int li = i * kMfmaThreads + t;
+        Bs[(li / BN) * kLdB + li % BN] = R.bs[i];
+      }
+    }
+  }
+};
+
+template <int BM, int BN, int BK, bool VEC>
+__global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
+    int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MT = WM / 32, NT = WN / 32;
+  static_assert(MT >= 1 && (NT == 1 || NT == 2 || NT == 4), "unsupported wave tile");
+  static_assert(BK % 8 == 0, "BK must be a multiple of 8 (two halves of 4-deep reads)");
+  using S = MfmaStage<BM, BN, BK, VEC>;
+  using BV = typename BVec<NT>::type;
+
+  __shared__ __attribute__((aligned(16))) float smem[2 * S::kStageFloats];
+
+  int tm, tn;
+  mfma_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int wm = wave / 2, wn = wave % 2;
+  const int h = lane / 32, c = lane % 32;
+
+  f32x16 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int ksteps = (K + BK - 1) / BK;
+  typename S::Regs R;
+  if (ksteps > 0) {
+    S::load(R, A, B, M, N, K, m0, n0, 0);
+    S::store(R, smem);
+  }
+  __syncthreads();
+
+  // Per-lane LDS offsets (floats) inside a stage.
+  const int a_off = (wm * WM + c) * S::kLdA + h * (BK / 2);
+  const int b_off = S::kAFloats + (h * (BK / 2)) * S::kLdB + wn * WN + NT * c;
+
+  for (int ks = 0; ks < ksteps; ++ks) {
+    const float* stage = smem + (ks & 1) * S::kStageFloats;
+    const bool more = (ks + 1) < ksteps;
+    if (more) S::load(R, A, B, M, N, K, m0, n0, (ks + 1) * BK);
+
+#pragma unroll
+    for (int q = 0; q < BK / 8; ++q) {
+      f32x4 av[MT];
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+        av[i] = *reinterpret_cast<const f32x4*>(stage + a_off + i * 32 * S::kLdA + 4 * q);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const BV bv = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + s) * S::kLdB);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j) {
+            float bj;
+            if constexpr (NT == 1) bj = bv; else bj = bv[j];
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], bj, acc[i][j], 0, 0, 0);
+          }
+        }
+      }
+    }
+
+    if (more) S::store(R, smem + ((ks + 1) & 1) * S::kStageFloats);
+    __syncthreads();
+  }
+
+  // Epilogue: C = alpha * acc + beta * C (C is not read when beta == 0).
+  const bool vec_store = VEC && (NT == 4) && ((N & 3) == 0);
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+      if (row >= M) continue;
+      const int col0 = n0 + wn * WN + NT * c;
+      float* crow = C + static_cast<int64_t>(row) * N;
+      float v[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) v[j] = alpha * acc[i][j][r];
+      if (vec_store && col0 + 3 < N) {
+        f32x4 o{v[0], v[NT > 1 ? 1 : 0], v[NT > 2 ? 2 : 0], v[NT > 3 ? 3 : 0]};
+        if (beta != 0.0f) o += beta * *reinterpret_cast<const f32x4*>(crow + col0);
+        *reinterpret_cast<f32x4*>(crow + col0) = o;
+      } else {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int col = col0 + j;
+          if (col < N) {
+            float o = v[j];
+            if (beta != 0.0f) o += beta * crow[col];
+            crow[col] = o;
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace mcke_amd

@@ -1,0 +1,185 @@
+"""The C-ABI library, without a GPU: it loads, exports every symbol the header
+declares, and rejects bad arguments before any device work (reference error
+conventions: kernels.hpp:78-86, bias_act.cu:208-229, reduce.cu:224-295,
+softmax.cu:177-199, gemm.cu:829-882).
+
+The argument-validation tests pass fake device pointers, which is only safe
+because every call here is rejected before a launch; they are skipped when a GPU
+is visible (the GPU suite repeats them with real buffers).
+"""
+from __future__ import annotations
+
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mcke_amd.h")
+
+
+def _declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mcke_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = _declared_functions()
+    for must in ("mcke_launch_gemm_f32", "mcke_launch_bias_act_f32", "mcke_launch_row_reduce_f32",
+                 "mcke_launch_row_reduce_ws_f32", "mcke_launch_row_softmax_f32",
+                 "mcke_row_reduce_workspace_bytes", "mcke_gemm_kernel_attrs", "mcke_last_error",
+                 "mcke_rt_stream_create", "mcke_rt_event_elapsed_ms", "mcke_rt_malloc"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(mcke):
+    L = mcke.lib()
+    for name in _declared_functions():
+        assert hasattr(L, name), f"{name} declared in mcke_amd.h but not exported"
+    out = subprocess.run(["nm", "-D", "--defined-only", mcke.library_path()],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s(mcke_\w+)", out))
+    assert set(_declared_functions()) <= exported
+    assert mcke.lib().mcke_abi_version() == 1
+
+
+def test_enum_values_match_reference(mcke):
+    assert [int(v) for v in mcke.Activation] == [0, 1, 2, 3]
+    assert [int(v) for v in mcke.ReduceKind] == [0, 1, 2]
+    assert [int(v) for v in mcke.ReduceVariant] == [0, 1, 2]
+    assert [int(v) for v in mcke.SoftmaxVariant] == [0, 1]
+    V = mcke.GemmVariant
+    assert (V.kNaive, V.kTiledSmem, V.kTiledRegBlock, V.kWarpTile, V.kCublasRef,
+            V.kWarpTileNoDbuf, V.kWarpTileVec4, V.kNaiveUncoalesced, V.kMfmaF32) == tuple(range(9))
+    assert [int(c) for c in mcke.StatusCode] == list(range(7))
+
+
+def test_host_generators_match_oracle(mcke, orc):
+    import numpy as np
+    for seed, lo, hi in ((0x6E33A, -1.0, 1.0), (3, 0.0, 1.0), (0xB1A5B1A5, -0.5, 0.5)):
+        assert np.array_equal(mcke.fill_random(10001, seed, lo, hi).view(np.uint32),
+                              orc.fill_random(10001, seed, lo, hi).view(np.uint32))
+    for seed, mu, sigma in ((1, 0.0, 1.0), (2, 0.0, 2.0), (3, 0.0, 0.02)):
+        assert np.array_equal(mcke.fill_normal(10001, seed, mu, sigma).view(np.uint32),
+                              orc.fill_normal(10001, seed, mu, sigma).view(np.uint32))
+
+
+def test_max_vector_width(mcke):
+    assert mcke.max_vector_width_f32(0x1000, 4096) == 4
+    assert mcke.max_vector_width_f32(0x1000, 4098) == 2
+    assert mcke.max_vector_width_f32(0x1008, 4096) == 2
+    assert mcke.max_vector_width_f32(0x1004, 4096) == 1
+    assert mcke.max_vector_width_f32(0x1000, 7) == 1
+
+
+def test_workspace_query(mcke):
+    TP = mcke.ReduceVariant.kTwoPass
+    assert mcke.row_reduce_workspace_bytes(8192, 8192, mcke.ReduceVariant.kWarpShuffle) == 0
+    assert mcke.row_reduce_workspace_bytes(0, 100, TP) == 0
+    assert mcke.row_reduce_workspace_bytes(8192, 8192, TP) == 8192 * 4          # split 1
+    assert mcke.row_reduce_workspace_bytes(1, 1 << 26, TP) == 2048 * 4          # full sum
+    assert mcke.row_reduce_workspace_bytes(64, 524288, TP) == 64 * 32 * 4
+    assert mcke.row_reduce_workspace_bytes(1, 1000, TP) == 4                    # short row
+
+
+def test_default_mfma_tile(mcke):
+    t = mcke.gemm_mfma_default_tile(8192, 8192, 8192)
+    assert t.astuple() == (256, 256, 32, 16, 16)
+    assert mcke.gemm_mfma_default_tile(2048, 2048, 2048).astuple() == (128, 128, 32, 8, 8)
+    assert mcke.gemm_mfma_default_tile(512, 512, 512).astuple() == (64, 64, 32, 4, 4)
+
+
+# ---------------------------------------------------------------------------
+# Argument validation with fake pointers (rejected before any launch)
+# ---------------------------------------------------------------------------
+def _no_gpu(mcke) -> bool:
+    try:
+        return mcke.device_count() == 0
+    except Exception:
+        return True
+
+
+@pytest.fixture()
+def cpu_only(mcke):
+    if not _no_gpu(mcke):
+        pytest.skip("a GPU is visible: tests/test_gpu_errors.py covers this with real buffers")
+    return mcke
+
+
+X, Y, B, W = 0x10000, 0x20000, 0x30000, 0x40000   # fake, 256-byte aligned
+
+
+def test_empty_extents_are_ok_without_launch(cpu_only):
+    m = cpu_only
+    assert m.launch_bias_act_f32(X, B, Y, 0, 10, 3, 4).ok()
+    assert m.launch_bias_act_f32(None, None, None, 5, 0, 3, 4).ok()
+    assert m.launch_row_reduce_f32(X, Y, 0, 5, 0, 1).ok()
+    assert m.launch_row_softmax_f32(X, Y, 7, 0, 1).ok()
+    assert m.launch_gemm_f32(X, B, Y, 0, 5, 5, 1.0, 0.0, m.GemmVariant.kMfmaF32,
+                             m.MFMA_TILES[0]).ok()
+    assert m.launch_activation_f32(X, Y, 0, 3, 4).ok()
+    assert m.launch_vector_add_f32(X, B, Y, 0).ok()
+
+
+def test_bias_act_rejections(cpu_only):
+    m = cpu_only
+    IA = m.StatusCode.kInvalidArgument
+    assert m.launch_bias_act_f32(X, None, Y, 4, 8, 3, 4).code == IA           # null bias
+    assert m.launch_bias_act_f32(None, B, Y, 4, 8, 3, 4).code == IA           # null x
+    assert m.launch_bias_act_f32(X, B, Y, -1, 8, 3, 4).code == IA             # negative
+    assert m.launch_bias_act_f32(X, B, Y, 4, 8, 3, 3).code == IA              # vw 3
+    st = m.launch_bias_act_f32(X, B, Y, 4, 6, 3, 4)                           # cols % vw
+    assert st.code == IA and "multiple of vector_width" in st.message
+    assert m.launch_bias_act_f32(X + 4, B, Y, 4, 8, 3, 4).code == IA          # misaligned x
+    assert m.launch_bias_act_f32(X, B + 8, Y, 4, 8, 3, 4).code == IA          # misaligned bias
+    assert m.launch_bias_act_f32(X, B, X, 4, 8, 3, 4).code == IA              # in place
+    assert m.launch_bias_act_f32(X, B, Y, 4, 8, 9, 4).code == IA              # bad act
+    assert m.launch_activation_f32(X, Y, 6, 3, 4).code == IA                  # n % vw
+
+
+def test_reduce_rejections(cpu_only):
+    m = cpu_only
+    IA = m.StatusCode.kInvalidArgument
+    TP = m.ReduceVariant.kTwoPass
+    st = m.launch_row_reduce_f32(X, Y, 4, 8, 0, TP)                           # 7-arg kTwoPass
+    assert st.code == m.StatusCode.kUnimplemented
+    assert m.launch_row_reduce_f32(X, Y, 4, 8, 0, TP, None, 0, None).code == IA
+    need = m.row_reduce_workspace_bytes(1, 1 << 20, TP)
+    assert m.launch_row_reduce_f32(X, Y, 1, 1 << 20, 0, TP, W, need - 4, None).code == IA
+    assert m.launch_row_reduce_f32(X, Y, -2, 8, 0, 1).code == IA
+    assert m.launch_row_reduce_f32(None, Y, 2, 8, 0, 1).code == IA
+    assert m.launch_row_reduce_f32(X, Y, 2, 8, 7, 1).code == IA               # bad kind
+    assert m.launch_row_reduce_f32(X, Y, 1 << 31, 8, 0, 1).code == IA         # rows > 2^31-1
+
+
+def test_softmax_rejections(cpu_only):
+    m = cpu_only
+    IA = m.StatusCode.kInvalidArgument
+    assert m.launch_row_softmax_f32(X, X, 4, 8, 1).code == IA
+    assert m.launch_row_softmax_f32(X, None, 4, 8, 1).code == IA
+    assert m.launch_row_softmax_f32(X, Y, -4, 8, 1).code == IA
+    assert m.launch_row_softmax_f32(X, Y, 1 << 31, 8, 1).code == IA
+    assert m.launch_row_softmax_f32(X, Y, 4, 8, 5).code == IA
+
+
+def test_gemm_rejections(cpu_only):
+    m = cpu_only
+    IA = m.StatusCode.kInvalidArgument
+    V, T = m.GemmVariant, m.GemmTile
+    good = m.MFMA_TILES[0]
+    assert m.launch_gemm_f32(X, B, X, 8, 8, 8, 1, 0, V.kMfmaF32, good).code == IA   # a == c
+    assert m.launch_gemm_f32(X, B, B, 8, 8, 8, 1, 0, V.kMfmaF32, good).code == IA   # b == c
+    assert m.launch_gemm_f32(X, B, Y, -8, 8, 8, 1, 0, V.kMfmaF32, good).code == IA
+    assert m.launch_gemm_f32(X, None, Y, 8, 8, 8, 1, 0, V.kMfmaF32, good).code == IA
+    assert m.launch_gemm_f32(X, B, Y, 1 << 31, 8, 8, 1, 0, V.kMfmaF32, good).code == IA
+    # unsupported (variant, tile) pairs: no fallback
+    assert m.launch_gemm_f32(X, B, Y, 8, 8, 8, 1, 0, V.kTiledSmem, T()).code == IA
+    assert m.launch_gemm_f32(X, B, Y, 8, 8, 8, 1, 0, V.kWarpTile, T(32, 32, 32, 1, 1)).code == IA
+    st = m.launch_gemm_f32(X, B, Y, 8, 8, 8, 1, 0, V.kMfmaF32, T(128, 128, 8, 8, 8))
+    assert st.code == IA and "no fallback" in st.message
+    assert m.launch_gemm_f32(X, B, Y, 8, 8, 8, 1, 0, V.kMfmaF32, T(100, 128, 8, 8, 8)).code == IA
+    assert m.launch_gemm_f32(X, B, Y, 8, 8, 8, 1, 0, 42, good).code == IA
+    # the ladder's 2-D grid caps the row tiles at 65535
+    assert m.launch_gemm_f32(X, B, Y, 65536 * 4 + 1, 8, 8, 1, 0, V.kNaive, T()).code == IA

@@ -1,0 +1,245 @@
+"""GPU parity: every launcher, through the C-ABI, against the CPU oracle.
+
+Bars (stated per test):
+  * golden "exact" cases: bit-for-bit (quarter-multiple inputs make every sum exact
+    in f32, whatever the summation order -- so MFMA and FMA paths alike must match);
+  * golden "approx" cases: rel 1e-6 + abs 1e-7 (the reference's fixture bar,
+    test_host_core.cpp:2447-2449), GELU with its cancellation floor abs 1e-6;
+  * seeded random inputs: the reference's mixed abs+rel tolerances
+    (reference.hpp:292-374) and BASELINE's stated ones.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests import golden_io
+from tests.gpu_util import (cfg_id, gemm_configs, run_activation, run_bias_act, run_gemm,
+                            run_reduce, run_softmax)
+
+pytestmark = pytest.mark.gpu
+
+CASES = golden_io.all_cases()
+
+
+def _golden_ids(kind):
+    return [c for c in CASES if c["kind"] == kind]
+
+
+# ---------------------------------------------------------------------------
+# Golden vectors
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("case", _golden_ids("bias_act"), ids=lambda c: c["name"])
+@pytest.mark.parametrize("vw", [1, 2, 4])
+def test_golden_bias_act(gpu, orc, case, vw):
+    I, A = case["ints"], case["arrays"]
+    if I["cols"] % vw:
+        pytest.skip("cols not a multiple of the vector width")
+    got = run_bias_act(gpu, A["x"], A["bias"], I["rows"], I["cols"], I["act"], vw)
+    want = A["expect"]
+    if case["mode"] == "exact":
+        assert np.array_equal(golden_io.bits(got), golden_io.bits(want))
+    else:
+        r = orc.compare(got, want, 1e-6, 1e-6)
+        assert r.ok, str(r)
+
+
+@pytest.mark.parametrize("case", _golden_ids("row_reduce"), ids=lambda c: c["name"])
+@pytest.mark.parametrize("variant", [0, 1, 2])
+def test_golden_row_reduce(gpu, orc, case, variant):
+    I, A = case["ints"], case["arrays"]
+    got = run_reduce(gpu, A["x"], I["rows"], I["cols"], I["kind"], variant)
+    assert np.array_equal(golden_io.bits(got), golden_io.bits(A["expect"]))
+
+
+@pytest.mark.parametrize("case", _golden_ids("row_softmax"), ids=lambda c: c["name"])
+@pytest.mark.parametrize("variant", [0, 1])
+def test_golden_softmax(gpu, orc, case, variant):
+    I, A = case["ints"], case["arrays"]
+    got = run_softmax(gpu, A["x"], I["rows"], I["cols"], variant)
+    r = orc.compare(got, A["expect"], 1e-6, 1e-7)
+    assert r.ok, str(r)
+
+
+@pytest.mark.parametrize("case", _golden_ids("gemm"), ids=lambda c: c["name"])
+def test_golden_gemm_all_variants(gpu, case):
+    I, A, F = case["ints"], case["arrays"], case["floats"]
+    for cfg in gemm_configs(gpu):
+        got = run_gemm(gpu, A["a"], A["b"], A["c"], I["m"], I["n"], I["k"], F["alpha"],
+                       F["beta"], *cfg)
+        assert np.array_equal(golden_io.bits(got), golden_io.bits(A["expect"])), cfg_id(cfg)
+
+
+# ---------------------------------------------------------------------------
+# Seeded random inputs
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
+@pytest.mark.parametrize("shape", [(37, 129), (64, 1024), (5, 4100)])
+def test_bias_act_random(gpu, orc, act, shape):
+    rows, cols = shape
+    x = orc.fill_normal(rows * cols, 0xB1A5AC7, 0.0, 2.0)
+    b = orc.fill_random(cols, 0xB1A5B1A5, -0.5, 0.5)
+    want = orc.bias_act(x, b, rows, cols, act)
+    for vw in (1, 2, 4):
+        if cols % vw:
+            continue
+        got = run_bias_act(gpu, x, b, rows, cols, act, vw)
+        if act in (0, 1):
+            assert np.array_equal(golden_io.bits(got), golden_io.bits(want)), vw
+        else:
+            r = orc.compare(got, want, 1e-6, 1e-6)
+            assert r.ok, f"vw={vw}: {r}"
+
+
+def test_bias_act_width_invariance_and_starved_grid(gpu, orc):
+    rows, cols = 300, 2048
+    x = orc.fill_normal(rows * cols, 5)
+    b = orc.fill_random(cols, 6, -0.5, 0.5)
+    y1 = run_bias_act(gpu, x, b, rows, cols, 3, 1)
+    y4 = run_bias_act(gpu, x, b, rows, cols, 3, 4)
+    y4s = run_bias_act(gpu, x, b, rows, cols, 3, 4, max_row_blocks=7)
+    assert np.array_equal(golden_io.bits(y1), golden_io.bits(y4))
+    assert np.array_equal(golden_io.bits(y4), golden_io.bits(y4s))
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
+def test_activation_unfused(gpu, orc, act):
+    n = 3 * 4096
+    x = orc.fill_normal(n, 11, 0.0, 3.0)
+    want = orc.bias_act(x, np.zeros(n, np.float32), 1, n, act)
+    got = run_activation(gpu, x, n, act, 4)
+    r = orc.compare(got, want, 1e-6, 1e-6)
+    assert r.ok, str(r)
+
+
+def _sum_abs_floor(x2d):
+    """Absolute floor for f32 sums of a row, from the magnitude of the terms
+    (the reference's rule, reference.hpp:312-321): 5e-5 at 4096 terms of
+    U[-1,1] (rms 0.577), scaled by the rows' rms and sqrt(cols/4096)."""
+    rms = float(np.sqrt(np.mean(np.square(x2d.astype(np.float64)))))
+    cols = x2d.shape[1]
+    return 5e-5 * (rms / 0.577) * max(1.0, np.sqrt(cols / 4096.0))
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("shape", [(1, 1), (3, 7), (17, 1000), (64, 4096), (2, 100003)])
+def test_row_reduce_random(gpu, orc, variant, shape):
+    rows, cols = shape
+    x = orc.fill_normal(rows * cols, 0x5EED12345)
+    for kind in (0, 1, 2):
+        got = run_reduce(gpu, x, rows, cols, kind, variant)
+        want = orc.row_reduce(x, rows, cols, kind)
+        if kind == 1:
+            assert np.array_equal(got, want)          # max: exact
+        else:
+            floor = _sum_abs_floor(x.reshape(rows, cols))
+            if kind == 2:
+                floor /= cols
+            r = orc.compare(got, want, 1e-5, floor)
+            assert r.ok, f"kind={kind}: {r}"
+
+
+def test_row_reduce_all_negative_and_inf_rows(gpu, orc):
+    x = np.array([[-5, -1, -9, -3], [-np.inf] * 4, [1, np.nan, 3, 2]], np.float32)
+    for variant in (0, 1, 2):
+        got = run_reduce(gpu, x, 3, 4, 1, variant)
+        assert got[0] == -1.0 and got[1] == -np.inf and got[2] == 3.0
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("cols", [1, 3, 17, 128, 131, 1024, 4096, 8192, 10000])
+def test_softmax_random(gpu, orc, variant, cols):
+    rows = 64 if cols <= 4096 else 8
+    x = orc.fill_normal(rows * cols, 0x50F7A11, 0.0, 2.0)
+    x[5 * cols] += 30.0                                  # a spike row
+    got = run_softmax(gpu, x, rows, cols, variant)
+    want = orc.row_softmax(x, rows, cols)
+    r = orc.compare(got, want, 1e-5, 1e-6)
+    assert r.ok, str(r)
+    sums = got.reshape(rows, cols).astype(np.float64).sum(axis=1)
+    assert np.max(np.abs(sums - 1.0)) <= 1e-5
+
+
+def test_softmax_overflow_ramp(gpu, orc):
+    """Logits 0..90: without the max subtraction expf overflows (softmax_bench.cpp:172-199)."""
+    cols = 1024
+    x = np.linspace(0.0, 90.0, cols, dtype=np.float32)
+    for variant in (0, 1):
+        got = run_softmax(gpu, x, 1, cols, variant)
+        assert np.isfinite(got).all()
+        r = orc.compare(got, orc.row_softmax(x, 1, cols), 1e-5, 1e-6)
+        assert r.ok, str(r)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (5, 7, 3), (129, 65, 257), (1, 64, 128),
+                                   (64, 1, 128), (33, 63, 1), (253, 253, 253), (256, 256, 256),
+                                   (300, 520, 36)])
+def test_gemm_random(gpu, orc, shape):
+    """The reference's validation shapes (gemm_bench.cpp:358-368), every variant."""
+    M, N, K = shape
+    a = orc.fill_random(M * K, 0x6E33A)
+    b = orc.fill_random(K * N, 0x8B10C)
+    c = np.zeros(M * N, np.float32)
+    want = orc.gemm(a, b, c, M, N, K)
+    rel, floor = orc.tol_gemm(K), orc.abs_tol_gemm(K)
+    for cfg in gemm_configs(gpu):
+        got = run_gemm(gpu, a, b, c, M, N, K, 1.0, 0.0, *cfg)
+        r = orc.compare(got, want, rel, floor)
+        assert r.ok, f"{cfg_id(cfg)}: {r}"
+
+
+def test_gemm_alpha_beta(gpu, orc):
+    """beta != 0 at 129x65x257 with alpha 0.5, beta 2 (gemm_bench.cpp:408-437)."""
+    M, N, K = 129, 65, 257
+    a = orc.fill_random(M * K, 0x6E33A)
+    b = orc.fill_random(K * N, 0x8B10C)
+    c = orc.fill_random(M * N, 0xC0FFEE)
+    want = orc.gemm(a, b, c, M, N, K, 0.5, 2.0)
+    rel, floor = orc.tol_gemm(K), orc.abs_tol_gemm(K) + 2e-7
+    for cfg in gemm_configs(gpu):
+        got = run_gemm(gpu, a, b, c, M, N, K, 0.5, 2.0, *cfg)
+        r = orc.compare(got, want, rel, floor)
+        assert r.ok, f"{cfg_id(cfg)}: {r}"
+
+
+def test_gemm_beta_zero_never_reads_c(gpu, orc):
+    M, N, K = 70, 90, 40
+    a = orc.fill_random(M * K, 1)
+    b = orc.fill_random(K * N, 2)
+    c = np.full(M * N, np.nan, np.float32)
+    want = orc.gemm(a, b, np.zeros(M * N, np.float32), M, N, K)
+    for cfg in gemm_configs(gpu):
+        got = run_gemm(gpu, a, b, c, M, N, K, 1.0, 0.0, *cfg)
+        assert not np.isnan(got).any(), cfg_id(cfg)
+        r = orc.compare(got, want, orc.tol_gemm(K), orc.abs_tol_gemm(K))
+        assert r.ok, f"{cfg_id(cfg)}: {r}"
+
+
+@pytest.mark.parametrize("size", [512, 1024])
+def test_gemm_quarter_exact_mfma(gpu, size):
+    """Quarter-multiple inputs: the exact product is representable in f32 and any
+    summation order reproduces it, so the MFMA path must match float64 bit for bit."""
+    rng = np.random.default_rng(size)
+    a = (rng.integers(-16, 17, size * size) * 0.25).astype(np.float32)
+    b = (rng.integers(-16, 17, size * size) * 0.25).astype(np.float32)
+    want = (a.reshape(size, size).astype(np.float64) @
+            b.reshape(size, size).astype(np.float64)).astype(np.float32).ravel()
+    for t in gpu.MFMA_TILES:
+        got = run_gemm(gpu, a, b, np.zeros(size * size, np.float32), size, size, size, 1.0,
+                       0.0, gpu.GemmVariant.kMfmaF32, t)
+        assert np.array_equal(golden_io.bits(got), golden_io.bits(want)), repr(t)
+
+
+def test_gemm_512_baseline_config(gpu, orc):
+    """512^3, U[-1,1) from the reference seeds, rel tol 1e-4."""
+    n = 512
+    a = orc.fill_random(n * n, 0x6E33A)
+    b = orc.fill_random(n * n, 0x8B10C)
+    c = np.zeros(n * n, np.float32)
+    want = orc.gemm(a, b, c, n, n, n)
+    t = gpu.gemm_mfma_default_tile(n, n, n)
+    got = run_gemm(gpu, a, b, c, n, n, n, 1.0, 0.0, gpu.GemmVariant.kMfmaF32, t)
+    r = orc.compare(got, want, 1e-4, orc.abs_tol_gemm(n))
+    assert r.ok, str(r)
+    r2 = orc.compare(got, want, orc.tol_gemm(n), orc.abs_tol_gemm(n))
+    assert r2.ok, str(r2)
