@@ -71,10 +71,15 @@ class Op:
         }
 
 
-def build_ops(m, stream):
+def build_ops(m, stream, only=None):
+    """The step's launches; `only` (a set of op-name prefixes) restricts the set,
+    and also enables the calibration op `copy_256mib` (a plain 256 MiB copy)."""
     D = m.DeviceBuffer
     ops, keep = [], []
     st = stream
+
+    def want(name):
+        return only is None or any(name.startswith(p) for p in only)
 
     def ck(status):
         if not status.ok():
@@ -82,40 +87,47 @@ def build_ops(m, stream):
 
     # --- GEMM 8192^3 (BASELINE configs[0] at its largest sweep size) ---------
     n = 8192
-    log("generating GEMM inputs (2 x 8192^2 U[-1,1))")
-    a = D.from_array(m.fill_random(n * n, 0x6E33A))
-    b = D.from_array(m.fill_random(n * n, 0x8B10C))
-    c = D.zeros(n * n)
-    tile = m.gemm_mfma_default_tile(n, n, n)
-    keep += [a, b, c]
-    ops.append(Op("gemm_mfma_f32", lambda: ck(m.launch_gemm_f32(
-        a, b, c, n, n, n, 1.0, 0.0, m.GemmVariant.kMfmaF32, tile, st)),
-        "mfma", 2 * n * n * n, "flop", f"{n}x{n}x{n} tile {tile.astuple()}"))
+    a = b = c = None
+    if want("gemm_mfma_f32"):
+        log("generating GEMM inputs (2 x 8192^2 U[-1,1))")
+        a = D.from_array(m.fill_random(n * n, 0x6E33A))
+        b = D.from_array(m.fill_random(n * n, 0x8B10C))
+        c = D.zeros(n * n)
+        tile = m.gemm_mfma_default_tile(n, n, n)
+        keep += [a, b, c]
+        ops.append(Op("gemm_mfma_f32", lambda: ck(m.launch_gemm_f32(
+            a, b, c, n, n, n, 1.0, 0.0, m.GemmVariant.kMfmaF32, tile, st)),
+            "mfma", 2 * n * n * n, "flop", f"{n}x{n}x{n} tile {tile.astuple()}"))
 
     # --- reductions --------------------------------------------
     R = C_ = 8192
-    log("generating reduce input (8192^2 N(0,1))")
-    xr = D.from_array(m.fill_normal(R * C_, 0x5EED12345))
-    outr = D(R * 4)
-    keep += [xr, outr]
-    red_bytes = (R * C_ + R) * 4
-    for kind, nm in ((m.ReduceKind.kSum, "row_sum"), (m.ReduceKind.kMax, "row_max")):
-        ops.append(Op(nm, (lambda kind=kind: ck(m.launch_row_reduce_f32(
-            xr, outr, R, C_, kind, m.ReduceVariant.kWarpShuffle, st))),
-            "hbm", red_bytes, "byte", f"{R}x{C_}"))
+    if want("row_sum") or want("row_max"):
+        log("generating reduce input (8192^2 N(0,1))")
+        xr = D.from_array(m.fill_normal(R * C_, 0x5EED12345))
+        outr = D(R * 4)
+        keep += [xr, outr]
+        red_bytes = (R * C_ + R) * 4
+        for kind, nm in ((m.ReduceKind.kSum, "row_sum"), (m.ReduceKind.kMax, "row_max")):
+            if want(nm):
+                ops.append(Op(nm, (lambda kind=kind: ck(m.launch_row_reduce_f32(
+                    xr, outr, R, C_, kind, m.ReduceVariant.kWarpShuffle, st))),
+                    "hbm", red_bytes, "byte", f"{R}x{C_}"))
     N26 = 1 << 26
-    log("generating full-sum input (2^26 U[0,1))")
-    xs = D.from_array(m.fill_random(N26, 0xF011, 0.0, 1.0))
-    wsb = m.row_reduce_workspace_bytes(1, N26, m.ReduceVariant.kTwoPass)
-    ws, outs = D(wsb), D(4)
-    keep += [xs, ws, outs]
-    ops.append(Op("full_sum", lambda: ck(m.launch_row_reduce_f32(
-        xs, outs, 1, N26, m.ReduceKind.kSum, m.ReduceVariant.kTwoPass, ws, wsb, st)),
-        "hbm", (N26 + 1) * 4, "byte", "1x2^26"))
+    if want("full_sum"):
+        log("generating full-sum input (2^26 U[0,1))")
+        xs = D.from_array(m.fill_random(N26, 0xF011, 0.0, 1.0))
+        wsb = m.row_reduce_workspace_bytes(1, N26, m.ReduceVariant.kTwoPass)
+        ws, outs = D(wsb), D(4)
+        keep += [xs, ws, outs]
+        ops.append(Op("full_sum", lambda: ck(m.launch_row_reduce_f32(
+            xs, outs, 1, N26, m.ReduceKind.kSum, m.ReduceVariant.kTwoPass, ws, wsb, st)),
+            "hbm", (N26 + 1) * 4, "byte", "1x2^26"))
 
     # --- softmax -----------------------------------------------
     rows = 32768
     for cols in (128, 1024, 4096):
+        if not want(f"softmax_c{cols}"):
+            continue
         log(f"generating softmax input (32768x{cols} N(0,4) + 1% spikes)")
         x = m.fill_normal(rows * cols, 0x50F7A11 + cols, 0.0, 2.0)
         rng = np.random.default_rng(cols)
@@ -129,6 +141,8 @@ def build_ops(m, stream):
 
     # --- bias + GELU(tanh) -------------------------------------
     for (br, bc) in ((16384, 4096), (4096, 1024)):
+        if not want(f"bias_gelu_{br}x{bc}"):
+            continue
         log(f"generating bias+GELU input ({br}x{bc})")
         dx = D.from_array(m.fill_normal(br * bc, 0xB1A5AC7 + br))
         db = D.from_array(m.fill_random(bc, 0xB1A5B1A5, -0.5, 0.5))
@@ -137,6 +151,14 @@ def build_ops(m, stream):
         ops.append(Op(f"bias_gelu_{br}x{bc}", (lambda dx=dx, db=db, dy=dy, br=br, bc=bc: ck(
             m.launch_bias_act_f32(dx, db, dy, br, bc, m.Activation.kGeluTanh, 4, st))),
             "hbm", (2 * br * bc + bc) * 4, "byte", f"{br}x{bc}"))
+
+    # --- calibration: a plain copy of known size (only when asked for) -------
+    if only is not None and want("copy_256mib"):
+        nc = 1 << 26
+        dx, dy = D.from_array(np.ones(nc, np.float32)), D(nc * 4)
+        keep += [dx, dy]
+        ops.append(Op("copy_256mib", lambda: ck(m.launch_activation_f32(
+            dx, dy, nc, m.Activation.kNone, 4, st)), "hbm", 2 * nc * 4, "byte", "2^26 floats"))
     m.device_synchronize()
     return ops, keep, (a, b, c, n)
 
@@ -247,7 +269,11 @@ def main(argv=None) -> int:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-sweep", action="store_true", help="skip the GEMM size sweep")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--only", default=None,
+                   help="comma-separated op-name prefixes to run (profiling); enables "
+                        "the copy_256mib calibration op")
     args = p.parse_args(argv)
+    only = set(args.only.split(",")) if args.only else None
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
@@ -258,7 +284,7 @@ def main(argv=None) -> int:
     info = m.require_gpu()
     log(f"device: {info.name.decode()} {info.arch.decode()} CUs={info.sm_count}")
     stream = m.Stream()
-    ops, keep, gemm_bufs = build_ops(m, stream)
+    ops, keep, gemm_bufs = build_ops(m, stream, only)
 
     log(f"warmup: {args.warmup} steps")
     run_steps(m, stream, ops, args.warmup, record=False)
@@ -269,10 +295,10 @@ def main(argv=None) -> int:
         log(f"{s['name']:>20s} {s['avg_ms']:.4f} ms  {s['achieved']:.1f} {s['unit']}  "
             f"({100 * s['frac']:.1f}% of {s['peak']})")
 
-    sweep = [] if args.no_sweep else gemm_sweep(m, stream)
+    sweep = [] if (args.no_sweep or only is not None) else gemm_sweep(m, stream)
     gemm = summaries[0]
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and gemm_bufs[0] is not None:
         log(f"cpu baseline: reference GEMM on a row slab (~{args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(m, gemm_bufs, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} TFLOP/s ({cpu['sample']})")
@@ -280,7 +306,7 @@ def main(argv=None) -> int:
     line = {
         "metric": METRIC,
         "value": gemm["achieved"],
-        "unit": "TFLOP/s",
+        "unit": gemm["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -299,8 +325,8 @@ def main(argv=None) -> int:
             "device": info.name.decode(),
         },
         "roofline": {
-            "bound": "mfma", "achieved": gemm["achieved"], "peak": PEAK_FP32_MFMA_TFLOPS,
-            "unit": "TFLOP/s", "frac": gemm["frac"], "traffic": None,
+            "bound": gemm["bound"], "achieved": gemm["achieved"], "peak": gemm["peak"],
+            "unit": gemm["unit"], "frac": gemm["frac"], "traffic": None,
         },
         "cpu_baseline": cpu,
         "ops": summaries,

@@ -217,15 +217,29 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
     const bool more = (ks + 1) < ksteps;
     if (more) S::load(R, A, B, M, N, K, m0, n0, (ks + 1) * BK);
 
+    // LDS -> register fragments, software-pipelined one MFMA step ahead: the
+    // reads for step (q, s+1) are issued before the MFMAs of step (q, s), so the
+    // LDS latency hides under 64 * MT * NT MFMA cycles instead of stalling them.
+    f32x4 av[MT], av_next[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      av[i] = *reinterpret_cast<const f32x4*>(stage + a_off + i * 32 * S::kLdA);
+    BV bv = *reinterpret_cast<const BV*>(stage + b_off);
 #pragma unroll
     for (int q = 0; q < BK / 8; ++q) {
-      f32x4 av[MT];
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-        av[i] = *reinterpret_cast<const f32x4*>(stage + a_off + i * 32 * S::kLdA + 4 * q);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const BV bv = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + s) * S::kLdB);
+        BV bv_next = bv;
+        if (s < 3) {
+          bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + s + 1) * S::kLdB);
+        } else if (q + 1 < BK / 8) {
+          bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + 4) * S::kLdB);
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+            av_next[i] = *reinterpret_cast<const f32x4*>(stage + a_off + i * 32 * S::kLdA +
+                                                         4 * (q + 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
 #pragma unroll
@@ -234,6 +248,12 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
             if constexpr (NT == 1) bj = bv; else bj = bv[j];
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], bj, acc[i][j], 0, 0, 0);
           }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        bv = bv_next;
+        if (s == 3 && q + 1 < BK / 8) {
+#pragma unroll
+          for (int i = 0; i < MT; ++i) av[i] = av_next[i];
         }
       }
     }

@@ -10,7 +10,7 @@
 //   kWarpShuffle one workgroup per row; wave64 butterfly, then one LDS stage
 //                across the 4 waves (1 barrier);
 //   kTwoPass     (rows x split) workgroups write partials to the caller's
-//                workspace, then one wave per row combines them in a fixed
+//                workspace, then one workgroup per row combines them in a fixed
 //                order.  With rows == 1 this is the full-tensor reduction.
 // Every variant is deterministic (no atomics): the same input gives the same
 // bits on every run.
@@ -33,9 +33,10 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kLoadUnroll = 4;
-// kTwoPass sizing: aim for ~8 workgroups per CU on a 256-CU part, but never give
-// a workgroup fewer than kMinColsPerBlock columns of one row.
-constexpr int64_t kTargetBlocks = 2048;
+// kTwoPass sizing: aim for ~4 workgroups per CU on a 256-CU part (measured best
+// for the full-tensor sum: fewer partials for pass 2, no tail), but never give a
+// workgroup fewer than kMinColsPerBlock columns of one row.
+constexpr int64_t kTargetBlocks = 1024;
 constexpr int64_t kMinColsPerBlock = 4096;
 constexpr int64_t kMaxSplit = 65535;
 
@@ -146,30 +147,36 @@ __global__ __launch_bounds__(kThreads) void row_reduce_pass1_kernel(
   if (threadIdx.x == 0) ws[r * split + s] = v;
 }
 
-// Pass 2: one wave per row folds the `split` partials in a fixed order.  Sums
-// are carried in double here: the partials are few and the second stage should
-// not add error on top of the first.
+// Pass 2: one workgroup folds the `split` partials of a row in a fixed order
+// (lane-strided, then a wave64 butterfly, then the 4 waves in order).  Sums are
+// carried in double: the partials are few and this stage should not add error
+// on top of the first.
 template <class Op, bool MEAN>
 __global__ __launch_bounds__(kThreads) void row_reduce_pass2_kernel(
-    const float* __restrict__ ws, float* __restrict__ out, int64_t rows, int64_t split,
-    int64_t cols) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
-  if (r >= rows) return;
-  const int lane = threadIdx.x % kWave;
+    const float* __restrict__ ws, float* __restrict__ out, int64_t split, int64_t cols) {
+  const int64_t r = blockIdx.x;
   const float* p = ws + r * split;
-  float v;
+  const int w = threadIdx.x / kWave;
   if constexpr (std::is_same_v<Op, SumOp>) {
+    __shared__ double part[kThreads / kWave];
     double acc = 0.0;
-    for (int64_t i = lane; i < split; i += kWave) acc += static_cast<double>(p[i]);
+    for (int64_t i = threadIdx.x; i < split; i += kThreads) acc += static_cast<double>(p[i]);
 #pragma unroll
     for (int m = kWave / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
-    v = static_cast<float>(MEAN ? acc / static_cast<double>(cols) : acc);
+    if ((threadIdx.x % kWave) == 0) part[w] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double t = part[0];
+#pragma unroll
+      for (int i = 1; i < kThreads / kWave; ++i) t += part[i];
+      out[r] = static_cast<float>(MEAN ? t / static_cast<double>(cols) : t);
+    }
   } else {
     float acc = Op::identity();
-    for (int64_t i = lane; i < split; i += kWave) acc = Op::apply(acc, p[i]);
-    v = Op::wave(acc);
+    for (int64_t i = threadIdx.x; i < split; i += kThreads) acc = Op::apply(acc, p[i]);
+    acc = block_combine_shfl<Op>(acc);
+    if (threadIdx.x == 0) out[r] = acc;
   }
-  if (lane == 0) out[r] = v;
 }
 
 int64_t two_pass_split(int64_t rows, int64_t cols) {
@@ -212,9 +219,8 @@ int launch_two_pass(const float* x, float* out, int64_t rows, int64_t cols, floa
   else
     row_reduce_pass1_kernel<Op, false><<<g1, kThreads, 0, st>>>(x, ws, cols, chunk, split);
   MCKE_LAUNCH_CHECK("row_reduce_pass1_kernel");
-  const int64_t g2 = (rows + (kThreads / kWave) - 1) / (kThreads / kWave);
-  row_reduce_pass2_kernel<Op, MEAN><<<static_cast<unsigned>(g2), kThreads, 0, st>>>(
-      ws, out, rows, split, cols);
+  row_reduce_pass2_kernel<Op, MEAN><<<static_cast<unsigned>(rows), kThreads, 0, st>>>(
+      ws, out, split, cols);
   MCKE_LAUNCH_CHECK("row_reduce_pass2_kernel");
   return ok();
 }
