@@ -204,6 +204,10 @@ int mcke_rt_host_free(void* ptr);
 /* kind: 0 host->device, 1 device->host, 2 device->device, 3 default (unified VA). */
 int mcke_rt_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream);
 int mcke_rt_memset_async(void* dst, int value, size_t bytes, void* stream);
+/* No reference counterpart: fills `count` 32-bit words with `value` using a
+ * kernel (usable under graph capture, unlike a memset node).  Used by the graph
+ * executor to poison its arena between runs. */
+int mcke_fill_u32_async(void* dst, uint32_t value, size_t count, void* stream);
 
 /* ---- host data generators (bench / test inputs) ----------------------------
  * The same map as the reference's fill_random (tests/reference.hpp:101-109):

@@ -92,6 +92,13 @@ __global__ __launch_bounds__(kThreads) void vector_add_kernel(const float* __res
     out[i] = a[i] + b[i];
 }
 
+__global__ __launch_bounds__(kThreads) void fill_u32_kernel(uint32_t* __restrict__ dst,
+                                                            uint32_t value, size_t count) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < count; i += stride)
+    dst[i] = value;
+}
+
 int validate_2d(const char* who, const float* x, const float* y, int64_t rows, int64_t cols,
                 int vw) {
   if (!x || !y) return invalid(std::string(who) + ": null pointer");
@@ -227,6 +234,18 @@ int mcke_launch_vector_add_f32(const float* a, const float* b, float* out, size_
   vector_add_kernel<<<static_cast<unsigned>(blocks), kThreads, 0,
                       static_cast<hipStream_t>(stream)>>>(a, b, out, n);
   MCKE_LAUNCH_CHECK("vector_add_kernel");
+  return ok();
+}
+
+int mcke_fill_u32_async(void* dst, uint32_t value, size_t count, void* stream) {
+  if (count == 0) return ok();
+  if (!dst) return invalid("fill_u32_async: null pointer");
+  if (!aligned(dst, 4)) return invalid("fill_u32_async: pointer not 4-byte aligned");
+  size_t blocks = (count + kThreads - 1) / kThreads;
+  if (blocks > 16384) blocks = 16384;
+  fill_u32_kernel<<<static_cast<unsigned>(blocks), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<uint32_t*>(dst), value, count);
+  MCKE_LAUNCH_CHECK("fill_u32_kernel");
   return ok();
 }
 

@@ -1,0 +1,317 @@
+"""Graph layer of the MCKE kernel layer, over the C-ABI in include/mcke_graph.h.
+
+Mirrors the reference's C++ Graph / GraphExecutor (reference
+include/mcke/graph/graph.hpp and executor.hpp): build a DAG of Gemm / BiasAct /
+Reduce / Softmax nodes, plan it onto HIP streams and one arena under a schedule
+and memory policy, replay it, and read back outputs, plan statistics, per-node
+timings, allocator statistics and the bitwise numerics gate.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import (HERE, GemmTile, GemmVariant, MckeError, Status, StatusCode, _sh,
+               lib as _amd_lib)
+
+HOST_LIB_PATH = os.path.join(HERE, "lib", "libmcke_host.so")
+
+
+class SchedulePolicy(enum.IntEnum):      # schedule.hpp:49
+    kSequential = 0
+    kLevelParallel = 1
+    kChainGreedy = 2
+
+
+class MemoryPolicy(enum.IntEnum):        # memory_plan.hpp
+    kAllocPerTensor = 0
+    kReuseTopoNaive = 1
+    kReuseSameStream = 2
+    kReuseHappensBefore = 3
+
+
+class AllocatorKind(enum.IntEnum):
+    kRaw = 0
+    kBuddy = 1
+
+
+class ExecutorOptions(C.Structure):
+    _fields_ = [("schedule", C.c_int32), ("memory", C.c_int32), ("num_streams", C.c_int32),
+                ("profile", C.c_int32), ("profile_slots", C.c_int32),
+                ("validate_numerics", C.c_int32), ("poison_buffers", C.c_int32),
+                ("poison_pattern", C.c_uint32)]
+
+
+class PlanInfo(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "num_nodes", "num_streams_used", "num_streams_requested", "num_events", "waits_raw",
+        "waits_dedup", "forkjoin_events", "arena_bytes", "naive_bytes", "buffers_used",
+        "total_flops", "total_bytes")]
+
+    def asdict(self):
+        return {n: int(getattr(self, n)) for n, _ in self._fields_}
+
+
+class NodeTiming(C.Structure):
+    _fields_ = [("node", C.c_uint32), ("stream_idx", C.c_int32), ("median_ms", C.c_double),
+                ("min_ms", C.c_double), ("flops", C.c_uint64), ("bytes", C.c_uint64),
+                ("samples", C.c_int32), ("name", C.c_char * 64)]
+
+
+class AllocatorStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "alloc_calls", "free_calls", "raw_malloc_calls", "raw_free_calls", "oom_events",
+        "deferred_reuses", "blocking_drains", "reuse_hits", "bytes_reserved", "bytes_in_use",
+        "bytes_requested", "peak_bytes_in_use", "largest_free_block")]
+
+    def asdict(self):
+        return {n: int(getattr(self, n)) for n, _ in self._fields_}
+
+
+_hl = None
+_VP, _U32, _U32P = C.c_void_p, C.c_uint32, C.POINTER(C.c_uint32)
+
+
+def host_lib() -> C.CDLL:
+    global _hl
+    if _hl is not None:
+        return _hl
+    _amd_lib()   # libmcke_amd.so first: libmcke_host.so links against it
+    if not os.path.exists(HOST_LIB_PATH):
+        raise RuntimeError(f"{HOST_LIB_PATH} is missing: run __graft_entry__.build()")
+    L = C.CDLL(HOST_LIB_PATH)
+    sig = {
+        "mcke_graph_last_error": (C.c_char_p, []),
+        "mcke_graph_create": (_VP, []),
+        "mcke_graph_destroy": (None, [_VP]),
+        "mcke_graph_add_input": (C.c_int, [_VP, C.POINTER(C.c_int64), C.c_int, C.c_char_p, _U32P]),
+        "mcke_graph_add_gemm": (C.c_int, [_VP, _U32, _U32, C.c_float, C.c_int, C.POINTER(GemmTile),
+                                          C.c_char_p, _U32P]),
+        "mcke_graph_add_bias_act": (C.c_int, [_VP, _U32, _U32, C.c_int, C.c_int, C.c_char_p, _U32P]),
+        "mcke_graph_add_reduce": (C.c_int, [_VP, _U32, C.c_int, C.c_int, C.c_char_p, _U32P]),
+        "mcke_graph_add_softmax": (C.c_int, [_VP, _U32, C.c_int, C.c_char_p, _U32P]),
+        "mcke_graph_mark_output": (C.c_int, [_VP, _U32]),
+        "mcke_graph_num_nodes": (C.c_int, [_VP, C.POINTER(C.c_uint64)]),
+        "mcke_graph_tensor_shape": (C.c_int, [_VP, _U32, C.POINTER(C.c_int64), C.POINTER(C.c_int)]),
+        "mcke_executor_create": (C.c_int, [_VP, C.c_int, C.POINTER(ExecutorOptions), C.POINTER(_VP)]),
+        "mcke_executor_destroy": (None, [_VP]),
+        "mcke_executor_plan": (C.c_int, [_VP]),
+        "mcke_executor_set_input": (C.c_int, [_VP, _U32, _VP, C.c_size_t]),
+        "mcke_executor_run_async": (C.c_int, [_VP]),
+        "mcke_executor_synchronize": (C.c_int, [_VP]),
+        "mcke_executor_read_tensor": (C.c_int, [_VP, _U32, _VP, C.c_size_t]),
+        "mcke_executor_plan_info": (C.c_int, [_VP, C.POINTER(PlanInfo)]),
+        "mcke_executor_collect_timings": (C.c_int, [_VP, C.POINTER(NodeTiming), C.c_size_t,
+                                                    C.POINTER(C.c_size_t)]),
+        "mcke_executor_validate_numerics": (C.c_int, [_VP, C.c_int, C.POINTER(C.c_int),
+                                                      C.POINTER(C.c_int), C.c_char_p, C.c_size_t]),
+        "mcke_executor_allocator_stats": (C.c_int, [_VP, C.POINTER(AllocatorStats)]),
+        "mcke_executor_stream": (C.c_int, [_VP, C.POINTER(_VP)]),
+        "mcke_executor_describe": (C.c_int, [_VP, C.c_char_p, C.c_size_t]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _hl = L
+    return L
+
+
+def host_library_path() -> str:
+    return HOST_LIB_PATH
+
+
+def _check(rc: int) -> None:
+    if rc == 0:
+        return
+    msg = host_lib().mcke_graph_last_error() or b""
+    if not msg:
+        msg = _amd_lib().mcke_last_error() or b""
+    raise MckeError(Status(StatusCode(rc), msg.decode()))
+
+
+class Graph:
+    """A DAG of kernel-backed ops over f32 tensors (reference Graph)."""
+
+    def __init__(self):
+        self.h = host_lib().mcke_graph_create()
+        self.names: dict[int, str] = {}
+
+    def _out(self, rc, out):
+        _check(rc)
+        return int(out.value)
+
+    def add_input(self, shape, name: str) -> int:
+        dims = (C.c_int64 * len(shape))(*shape)
+        out = C.c_uint32()
+        t = self._out(host_lib().mcke_graph_add_input(self.h, dims, len(shape), name.encode(),
+                                                      C.byref(out)), out)
+        self.names[t] = name
+        return t
+
+    def add_gemm(self, a: int, b: int, name: str, variant=GemmVariant.kMfmaF32,
+                 tile: GemmTile | None = None, alpha: float = 1.0) -> int:
+        out = C.c_uint32()
+        tp = C.byref(tile) if tile is not None else None
+        return self._out(host_lib().mcke_graph_add_gemm(self.h, a, b, alpha, int(variant), tp,
+                                                        name.encode(), C.byref(out)), out)
+
+    def add_bias_act(self, x: int, bias: int, name: str, act=3, vector_width: int = 0) -> int:
+        out = C.c_uint32()
+        return self._out(host_lib().mcke_graph_add_bias_act(self.h, x, bias, int(act), vector_width,
+                                                            name.encode(), C.byref(out)), out)
+
+    def add_reduce(self, x: int, name: str, kind=0, variant=1) -> int:
+        out = C.c_uint32()
+        return self._out(host_lib().mcke_graph_add_reduce(self.h, x, int(kind), int(variant),
+                                                          name.encode(), C.byref(out)), out)
+
+    def add_softmax(self, x: int, name: str, variant=1) -> int:
+        out = C.c_uint32()
+        return self._out(host_lib().mcke_graph_add_softmax(self.h, x, int(variant), name.encode(),
+                                                           C.byref(out)), out)
+
+    def mark_output(self, t: int) -> None:
+        _check(host_lib().mcke_graph_mark_output(self.h, t))
+
+    def shape(self, t: int) -> tuple:
+        dims = (C.c_int64 * 5)()
+        rank = C.c_int()
+        _check(host_lib().mcke_graph_tensor_shape(self.h, t, dims, C.byref(rank)))
+        return tuple(int(dims[i]) for i in range(rank.value))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            host_lib().mcke_graph_destroy(self.h)
+            self.h = None
+
+
+@dataclass
+class NumericsResult:
+    passed: bool
+    configs_compared: int
+    detail: str
+
+
+class Executor:
+    """GraphExecutor over a Graph (which it consumes)."""
+
+    def __init__(self, graph: Graph, allocator=AllocatorKind.kBuddy,
+                 schedule=SchedulePolicy.kChainGreedy, memory=MemoryPolicy.kReuseHappensBefore,
+                 num_streams: int = 4, profile: bool = False, profile_slots: int = 32,
+                 validate_numerics: bool = False, poison_buffers: bool = False):
+        opts = ExecutorOptions(int(schedule), int(memory), num_streams, int(profile), profile_slots,
+                               int(validate_numerics), int(poison_buffers), 0)
+        h = _VP()
+        _check(host_lib().mcke_executor_create(graph.h, int(allocator), C.byref(opts), C.byref(h)))
+        graph.h = None            # consumed
+        self.h = h.value
+
+    def plan(self) -> None:
+        _check(host_lib().mcke_executor_plan(self.h))
+
+    def set_input(self, t: int, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr, dtype=np.float32)
+        _check(host_lib().mcke_executor_set_input(self.h, t, arr.ctypes.data, arr.nbytes))
+
+    def run_async(self) -> None:
+        _check(host_lib().mcke_executor_run_async(self.h))
+
+    def synchronize(self) -> None:
+        _check(host_lib().mcke_executor_synchronize(self.h))
+
+    def run_sync(self) -> None:
+        self.run_async()
+        self.synchronize()
+
+    def read(self, t: int, numel: int) -> np.ndarray:
+        out = np.empty(numel, dtype=np.float32)
+        _check(host_lib().mcke_executor_read_tensor(self.h, t, out.ctypes.data, out.nbytes))
+        return out
+
+    def plan_info(self) -> dict:
+        info = PlanInfo()
+        _check(host_lib().mcke_executor_plan_info(self.h, C.byref(info)))
+        return info.asdict()
+
+    def timings(self) -> list[dict]:
+        n = C.c_size_t()
+        _check(host_lib().mcke_executor_collect_timings(self.h, None, 0, C.byref(n)))
+        arr = (NodeTiming * max(1, n.value))()
+        _check(host_lib().mcke_executor_collect_timings(self.h, arr, n.value, C.byref(n)))
+        return [{"node": t.node, "name": t.name.decode(), "stream": t.stream_idx,
+                 "median_ms": t.median_ms, "min_ms": t.min_ms, "flops": t.flops,
+                 "bytes": t.bytes, "samples": t.samples} for t in arr[:n.value]]
+
+    def validate_numerics(self, repeats: int = 3) -> NumericsResult:
+        passed, cfgs = C.c_int(), C.c_int()
+        buf = C.create_string_buffer(2048)
+        _check(host_lib().mcke_executor_validate_numerics(self.h, repeats, C.byref(passed),
+                                                          C.byref(cfgs), buf, 2048))
+        return NumericsResult(bool(passed.value), cfgs.value, buf.value.decode())
+
+    def allocator_stats(self) -> dict:
+        s = AllocatorStats()
+        _check(host_lib().mcke_executor_allocator_stats(self.h, C.byref(s)))
+        return s.asdict()
+
+    def stream(self) -> int:
+        s = _VP()
+        _check(host_lib().mcke_executor_stream(self.h, C.byref(s)))
+        return s.value
+
+    def describe(self) -> str:
+        buf = C.create_string_buffer(1 << 16)
+        _check(host_lib().mcke_executor_describe(self.h, buf, 1 << 16))
+        return buf.value.decode()
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            host_lib().mcke_executor_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def mlp_block(tokens: int, d_model: int, d_ff: int, gemm_variant=GemmVariant.kMfmaF32):
+    """BASELINE config 5's main chain: H = GELU(X W1 + b1); Z = H W2 + b2; softmax(Z)
+    (the reference's transformer_block, graph_bench.cpp:199-215, plus the b2 node)."""
+    g = Graph()
+    x = g.add_input((tokens, d_model), "x")
+    w1 = g.add_input((d_model, d_ff), "W1")
+    b1 = g.add_input((d_ff,), "b1")
+    w2 = g.add_input((d_ff, d_model), "W2")
+    b2 = g.add_input((d_model,), "b2")
+    g1 = g.add_gemm(x, w1, "gemm1", gemm_variant)
+    h = g.add_bias_act(g1, b1, "bias_gelu", act=3)
+    g2 = g.add_gemm(h, w2, "gemm2", gemm_variant)
+    z = g.add_bias_act(g2, b2, "bias_add", act=0)
+    y = g.add_softmax(z, "softmax")
+    g.mark_output(y)
+    return g, {"x": x, "W1": w1, "b1": b1, "W2": w2, "b2": b2, "gemm1": g1, "h": h, "gemm2": g2,
+               "z": z, "y": y}
+
+
+def gemm_fanout(branches: int, depth: int, n: int, gemm_variant=GemmVariant.kMfmaF32):
+    """`branches` independent chains of `depth` n^3 GEMMs: chain k is
+    C_k0 = X_k W, C_kd = C_k(d-1) W (the reference's fanout topology,
+    graph_bench.cpp:176-194, with GEMM nodes)."""
+    g = Graph()
+    w = g.add_input((n, n), "W")
+    xs, outs = [], []
+    for k in range(branches):
+        cur = g.add_input((n, n), f"x{k}")
+        xs.append(cur)
+        for d in range(depth):
+            cur = g.add_gemm(cur, w, f"b{k}g{d}", gemm_variant)
+        g.mark_output(cur)
+        outs.append(cur)
+    return g, {"W": w, "xs": xs, "outs": outs}

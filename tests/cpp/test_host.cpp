@@ -1,0 +1,627 @@
+// test_host.cpp -- CPU tests of the C++ host layers (no GPU needed).
+//
+// Covers: Status/StatusOr, GemmTile validity and the CDNA occupancy model, the
+// double-buffer schedule, the online-softmax algebra, the kernels.hpp launchers'
+// argument rejection (fake pointers, only when no GPU is visible), Shape, the
+// graph (finalize, depth/ALAP/slack, dead nodes, live ranges), the three stream
+// policies with their event and wait counts, happens-before, the memory planner
+// (exact bytes, unsafe arm flagged by the race verifier, random-DAG fuzz) and the
+// buddy allocator on host memory with fake streams.  Expected values are derived
+// in the comments next to each check.
+#include <cmath>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <random>
+#include <set>
+
+#include "check.hpp"
+#include "mcke/graph/executor.hpp"
+#include "mcke/graph/graph.hpp"
+#include "mcke/graph/memory_plan.hpp"
+#include "mcke/graph/schedule.hpp"
+#include "mcke/kernels/kernels.hpp"
+#include "mcke/kernels/softmax_online.hpp"
+#include "mcke/memory/buddy_allocator.hpp"
+#include "mcke/profiling/profiler.hpp"
+
+using namespace mcke;
+namespace K = mcke::kernels;
+
+// ---------------------------------------------------------------------------
+TEST(status_and_statusor) {
+  CHECK(OkStatus().ok());
+  const Status s = InvalidArgumentError("bad");
+  CHECK(!s.ok() && s.code() == StatusCode::kInvalidArgument && s.to_string() == "InvalidArgument: bad");
+  StatusOr<int> v = 7;
+  CHECK(v.ok() && *v == 7);
+  StatusOr<int> e = UnimplementedError("x");
+  CHECK(!e.ok() && e.status().code() == StatusCode::kUnimplemented);
+  CHECK(static_cast<int>(StatusCode::kDeviceError) == MCKE_STATUS_DEVICE_ERROR);
+  auto f = []() -> Status {
+    MCKE_ASSIGN_OR_RETURN(int a, StatusOr<int>(3));
+    MCKE_ASSIGN_OR_RETURN(int b, StatusOr<int>(InternalError("stop")));
+    return a + b > 0 ? OkStatus() : InternalError("unreachable");
+  };
+  CHECK(f().code() == StatusCode::kInternal);
+}
+
+// ---------------------------------------------------------------------------
+TEST(gemm_tile_validity_wave64) {
+  CHECK_EQ(K::threads_per_block(K::GemmTile{}), 256);
+  CHECK(K::tile_is_self_consistent(K::GemmTile{}));
+  CHECK(K::tile_is_self_consistent(K::GemmTile{32, 32, 32, 1, 1}));        // 1024 lanes
+  CHECK(!K::tile_is_self_consistent(K::GemmTile{16, 16, 8, 4, 4}));        // 16 lanes: not a wave
+  // 64x32 with 4x4: (16 x 8) = 128 lanes (2 waves); bm*bk = 512 and bk*bn = 256 both divide by 128.
+  CHECK(K::tile_is_self_consistent(K::GemmTile{64, 32, 8, 4, 4}));
+  CHECK(K::threads_per_block(K::GemmTile{64, 32, 8, 4, 4}) == 128);
+  // 32x32 with 4x4: 64 lanes, but bk*bn = 8*32 = 256 and bm*bk = 256 divide: valid;
+  // 32x16 with 4x4: 32 lanes, half a wave: invalid.
+  CHECK(K::tile_is_self_consistent(K::GemmTile{32, 32, 8, 4, 4}));
+  CHECK(!K::tile_is_self_consistent(K::GemmTile{32, 16, 8, 4, 4}));
+  CHECK(!K::tile_is_self_consistent(K::GemmTile{128, 128, 8, 0, 8}));
+  CHECK(!K::tile_is_self_consistent(K::GemmTile{100, 128, 8, 8, 8}));      // 100 % 8 != 0
+  for (const auto& t : {K::GemmTile{256, 256, 32, 16, 16}, K::GemmTile{256, 256, 16, 16, 16},
+                        K::GemmTile{128, 128, 32, 8, 8}, K::GemmTile{128, 128, 16, 8, 8},
+                        K::GemmTile{64, 64, 32, 4, 4}}) {
+    CHECK(K::tile_is_self_consistent(t));
+    CHECK_EQ(K::threads_per_block(t), 256);
+    CHECK(K::gemm_tile_is_supported(K::GemmVariant::kMfmaF32, t));
+    CHECK(!K::gemm_tile_is_supported(K::GemmVariant::kWarpTile, t));
+  }
+  CHECK(!K::gemm_tile_is_supported(K::GemmVariant::kMfmaF32, K::GemmTile{}));
+  CHECK(K::gemm_tile_is_supported(K::GemmVariant::kWarpTile, K::GemmTile{}));
+  CHECK(!K::gemm_tile_is_supported(K::GemmVariant::kTiledSmem, K::GemmTile{}));
+  CHECK(K::gemm_tile_is_supported(K::GemmVariant::kTiledSmem, K::GemmTile{32, 32, 32, 1, 1}));
+  CHECK(K::gemm_tile_is_supported(K::GemmVariant::kNaive, K::GemmTile{1, 2, 3, 4, 5}));   // ignores the tile
+  CHECK(K::gemm_tile_is_supported(K::GemmVariant::kCublasRef, K::GemmTile{1, 2, 3, 4, 5}));
+  // smem: (bk*(bm+pad) + bk*bn) floats, doubled when double-buffered.
+  CHECK_EQ(K::smem_bytes(K::GemmTile{}, false), std::size_t{8192});
+  CHECK_EQ(K::smem_bytes(K::GemmTile{}, true, 4), std::size_t{(8 * 132 + 8 * 128) * 4 * 2});
+  CHECK_EQ(static_cast<int>(K::GemmVariant::kMfmaF32), 8);
+}
+
+TEST(dbuf_schedule_exhaustive) {
+  for (std::int64_t n = 0; n <= 200; ++n) {
+    const auto s = K::dbuf_schedule(n);
+    CHECK_EQ(s.pair_iters * 2 + (s.has_tail ? 1 : 0), n);
+    CHECK(s.has_tail == (n % 2 == 1));
+  }
+  CHECK_EQ(K::dbuf_schedule(-3).pair_iters, 0);
+}
+
+TEST(occupancy_model_cdna) {
+  const DeviceInfo d = mi355x_device_info();
+  // 256 lanes = 4 waves = 1 wave per SIMD per workgroup.
+  // 512 VGPRs (the 256x256 MFMA tile): 512/512 = 1 wave per SIMD -> 1 workgroup;
+  // LDS 139264 B rounds to 139264 (512-multiple) -> 160K/139264 = 1.
+  auto e = K::occupancy_blocks_per_sm(d, 256, 512, 139264);
+  CHECK_EQ(e.blocks_per_sm, 1);
+  CHECK(e.tied);   // registers and LDS both allow exactly 1
+  // 168 VGPRs -> round to 168 -> 512/168 = 3 waves per SIMD; LDS 69632 -> 2 per CU.
+  e = K::occupancy_blocks_per_sm(d, 256, 168, 69632);
+  CHECK_EQ(e.by_registers, 3);
+  CHECK_EQ(e.by_smem, 2);
+  CHECK_EQ(e.blocks_per_sm, 2);
+  CHECK(e.limiter == K::OccupancyLimiter::kSharedMemory);
+  CHECK(std::fabs(e.occupancy - 512.0 / 2048.0) < 1e-12);
+  // No LDS, 32 VGPRs: registers allow 512/32 = 16 -> capped at 8 waves per SIMD;
+  // lanes cap 2048/256 = 8 blocks; 8 ties with registers -> the lanes cap is reported.
+  e = K::occupancy_blocks_per_sm(d, 256, 32, 0);
+  CHECK_EQ(e.by_registers, 8);
+  CHECK_EQ(e.by_threads, 8);
+  CHECK_EQ(e.blocks_per_sm, 8);
+  CHECK(e.limiter == K::OccupancyLimiter::kThreadsPerSm && e.tied);
+  // 1024-lane workgroup = 16 waves = 4 per SIMD: 100 VGPRs -> round 104 -> 4 waves/SIMD -> 1 block.
+  e = K::occupancy_blocks_per_sm(d, 1024, 100, 0);
+  CHECK_EQ(e.by_registers, 1);
+  CHECK_EQ(e.blocks_per_sm, 1);
+  // Will not launch: LDS beyond the CU, or more lanes than a workgroup may have.
+  CHECK(K::occupancy_blocks_per_sm(d, 256, 64, 200 * 1024).limiter == K::OccupancyLimiter::kInvalid);
+  CHECK(K::occupancy_blocks_per_sm(d, 2048, 64, 0).blocks_per_sm == 0);
+  CHECK(K::occupancy_blocks_per_sm(DeviceInfo{}, 256, 64, 0).blocks_per_sm == 0);
+}
+
+// ---------------------------------------------------------------------------
+TEST(online_softmax_algebra) {
+  const K::OnlineState id = K::online_identity();
+  const K::OnlineState e = K::online_combine(id, id);
+  CHECK(!std::isnan(e.m) && !std::isnan(e.d) && e.d == 0.0f);
+  std::mt19937 rng(3);
+  std::normal_distribution<float> nd(0.f, 5.f);
+  for (int n : {1, 2, 17, 64, 1000}) {
+    std::vector<float> x(n);
+    for (auto& v : x) v = nd(rng);
+    K::OnlineState s = id;
+    for (float v : x) s = K::online_update(s, v);
+    double m = -INFINITY;
+    for (float v : x) m = std::max(m, static_cast<double>(v));
+    double d = 0;
+    for (float v : x) d += std::exp(static_cast<double>(v) - m);
+    CHECK(s.m == static_cast<float>(m));
+    CHECK(std::fabs(s.d - d) <= 1e-5 * d);
+    // split into two halves and combine (both orders)
+    K::OnlineState a = id, b = id;
+    for (int i = 0; i < n; ++i) (i < n / 2 ? a : b) = K::online_update(i < n / 2 ? a : b, x[i]);
+    const K::OnlineState ab = K::online_combine(a, b), ba = K::online_combine(b, a);
+    CHECK(ab.m == ba.m && std::fabs(ab.d - ba.d) <= 1e-6f * ab.d);
+    CHECK(std::fabs(ab.d - d) <= 1e-5 * d);
+  }
+}
+
+// ---------------------------------------------------------------------------
+static bool no_gpu() { return device_count() == 0; }
+
+TEST(launchers_reject_bad_arguments_without_launching) {
+  if (!no_gpu()) {
+    std::printf("  (skipped: a GPU is visible)\n");
+    return;
+  }
+  auto* X = reinterpret_cast<float*>(0x10000);
+  auto* Y = reinterpret_cast<float*>(0x20000);
+  auto* B = reinterpret_cast<float*>(0x30000);
+  rt::StreamHandle s{};
+  CHECK(K::launch_bias_act_f32(X, B, Y, 0, 8, K::Activation::kGeluTanh, 4, s).ok());
+  CHECK(K::launch_bias_act_f32(X, B, X, 4, 8, K::Activation::kGeluTanh, 4, s).code() == StatusCode::kInvalidArgument);
+  CHECK(K::launch_bias_act_f32(X, B, Y, 4, 6, K::Activation::kGeluTanh, 4, s).code() == StatusCode::kInvalidArgument);
+  CHECK(K::launch_row_reduce_f32(X, Y, 4, 8, K::ReduceKind::kSum, K::ReduceVariant::kTwoPass, s).code() ==
+        StatusCode::kUnimplemented);
+  CHECK(K::launch_row_softmax_f32(X, X, 4, 8, K::SoftmaxVariant::kOnlineOnePass, s).code() ==
+        StatusCode::kInvalidArgument);
+  CHECK(K::launch_gemm_f32(X, B, X, 8, 8, 8, 1.f, 0.f, K::GemmVariant::kMfmaF32, K::GemmTile{256, 256, 32, 16, 16}, s)
+            .code() == StatusCode::kInvalidArgument);
+  const Status st = K::launch_gemm_f32(X, B, Y, 8, 8, 8, 1.f, 0.f, K::GemmVariant::kTiledSmem, K::GemmTile{}, s);
+  CHECK(st.code() == StatusCode::kInvalidArgument && st.message().find("no fallback") != std::string::npos);
+  CHECK(K::max_vector_width_f32(X, 4096) == 4 && K::max_vector_width_f32(X, 4094) == 2);
+  CHECK(K::row_reduce_workspace_bytes(1, 1 << 26, K::ReduceVariant::kTwoPass) == 1024 * 4);
+  CHECK(K::mfma_default_tile(8192, 8192, 8192).bm == 256);
+}
+
+// ---------------------------------------------------------------------------
+TEST(shape_basics) {
+  const Shape s{2, 3, 4};
+  CHECK(s.rank() == 3 && s.numel() == 24 && s.rows() == 6 && s.cols() == 4);
+  CHECK(s.stride(0) == 12 && s.stride(1) == 4 && s.stride(2) == 1 && s.is_contiguous());
+  CHECK(s.bytes(DType::kF32) == 96 && s.to_string() == "[2,3,4]");
+  const dim_t idx[3] = {1, 2, 3};
+  CHECK(s.offset_of(idx) == 23);
+  CHECK(Shape{5}.rows() == 1 && Shape{5}.cols() == 5);
+}
+
+// ---------------------------------------------------------------------------
+// Graph builders (the reference's bench topologies, graph_bench.cpp:120-215).
+static OpPtr bias_act(BiasActParams::Act a = BiasActParams::Act::kGeluTanh) {
+  BiasActParams p;
+  p.act = a;
+  return std::make_unique<BiasActOp>(p);
+}
+
+struct Built {
+  Graph g;
+  std::vector<TensorId> inputs, outputs;
+};
+
+static Built chain(int n, dim_t rows, dim_t cols) {
+  Built b;
+  const TensorId x = *b.g.add_input(Shape{rows, cols}, DType::kF32, "x");
+  const TensorId bi = *b.g.add_input(Shape{cols}, DType::kF32, "bias");
+  b.inputs = {x, bi};
+  TensorId cur = x;
+  for (int i = 0; i < n; ++i) cur = (*b.g.add_node(bias_act(), {cur, bi}, "n" + std::to_string(i)))[0];
+  (void)b.g.mark_output(cur);
+  b.outputs = {cur};
+  (void)b.g.finalize();
+  return b;
+}
+
+static Built fanout(int branches, int depth, dim_t rows, dim_t cols) {
+  Built b;
+  const TensorId x = *b.g.add_input(Shape{rows, cols}, DType::kF32, "x");
+  const TensorId bi = *b.g.add_input(Shape{cols}, DType::kF32, "bias");
+  b.inputs = {x, bi};
+  for (int k = 0; k < branches; ++k) {
+    TensorId cur = x;
+    for (int d = 0; d < depth; ++d)
+      cur = (*b.g.add_node(bias_act(), {cur, bi}, "b" + std::to_string(k) + "n" + std::to_string(d)))[0];
+    (void)b.g.mark_output(cur);
+    b.outputs.push_back(cur);
+  }
+  (void)b.g.finalize();
+  return b;
+}
+
+// a -> {b, c} -> d (diamond)
+static Built diamond(dim_t rows, dim_t cols) {
+  Built b;
+  const TensorId x = *b.g.add_input(Shape{rows, cols}, DType::kF32, "x");
+  const TensorId bi = *b.g.add_input(Shape{cols}, DType::kF32, "bias");
+  const TensorId a = (*b.g.add_node(bias_act(), {x, bi}, "a"))[0];
+  const TensorId l = (*b.g.add_node(bias_act(), {a, bi}, "l"))[0];
+  const TensorId r = (*b.g.add_node(std::make_unique<ReduceOp>(ReduceParams{}), {a}, "r"))[0];
+  GemmParams gp;
+  gp.variant = K::GemmVariant::kMfmaF32;
+  gp.auto_tile = true;
+  // d = l (rows x cols) times a [cols x cols] weight: use a second input.
+  const TensorId w = *b.g.add_input(Shape{cols, cols}, DType::kF32, "w");
+  const TensorId d = (*b.g.add_node(std::make_unique<GemmOp>(gp), {l, w}, "d"))[0];
+  (void)b.g.mark_output(d);
+  (void)b.g.mark_output(r);
+  b.outputs = {d, r};
+  (void)b.g.finalize();
+  return b;
+}
+
+TEST(graph_finalize_depths_and_dead_nodes) {
+  Built b = diamond(64, 64);
+  CHECK(b.g.finalized());
+  // nodes: 0 a (depth 0), 1 l (1), 2 r (1), 3 d (2)
+  CHECK(b.g.node(0).depth == 0 && b.g.node(1).depth == 1 && b.g.node(2).depth == 1 && b.g.node(3).depth == 2);
+  // r's only successor... r has none; its ALAP depth is the critical depth (2), slack 1.
+  CHECK(b.g.node(2).alap_depth == 2 && b.g.node(2).slack == 1);
+  CHECK(b.g.node(1).slack == 0 && b.g.node(0).slack == 0);
+  CHECK(b.g.dead_nodes().empty());
+  CHECK(*b.g.max_level_width() == 2);
+  CHECK(b.g.node(3).preds == std::vector<NodeId>{1});
+  CHECK((b.g.node(0).succs == std::vector<NodeId>{1, 2}));
+
+  // A node that reaches no output is dead.
+  Graph g;
+  const TensorId x = *g.add_input(Shape{4, 4}, DType::kF32, "x");
+  const TensorId bi = *g.add_input(Shape{4}, DType::kF32, "b");
+  const TensorId y = (*g.add_node(bias_act(), {x, bi}, "live"))[0];
+  (void)(*g.add_node(bias_act(), {x, bi}, "dead"));
+  CHECK_OK(g.mark_output(y));
+  CHECK_OK(g.finalize());
+  CHECK(g.dead_nodes() == std::vector<NodeId>{1});
+}
+
+TEST(graph_errors) {
+  Graph g;
+  CHECK(g.finalize().code() == StatusCode::kFailedPrecondition);   // no nodes
+  CHECK(g.add_input(Shape{0, 4}, DType::kF32, "bad").status().code() == StatusCode::kInvalidArgument);
+  const TensorId x = *g.add_input(Shape{4, 4}, DType::kF32, "x");
+  const TensorId bi = *g.add_input(Shape{5}, DType::kF32, "b");
+  CHECK(g.add_node(bias_act(), {x, bi}, "mismatch").status().code() == StatusCode::kInvalidArgument);
+  CHECK(g.add_node(bias_act(), {x, 99}, "oob").status().code() == StatusCode::kInvalidArgument);
+  CHECK(g.add_node(nullptr, {x}, "null").status().code() == StatusCode::kInvalidArgument);
+  const TensorId b4 = *g.add_input(Shape{4}, DType::kF32, "b4");
+  (void)(*g.add_node(bias_act(), {x, b4}, "ok"));
+  CHECK(g.finalize().code() == StatusCode::kInvalidArgument);      // no outputs
+  GemmParams gp;
+  gp.beta = 1.0f;
+  CHECK(g.add_node(std::make_unique<GemmOp>(gp), {x, x}, "beta").status().code() == StatusCode::kUnimplemented);
+  GemmParams bad_tile;
+  bad_tile.variant = K::GemmVariant::kTiledSmem;   // default tile is not (32,32,32,1,1)
+  CHECK(g.add_node(std::make_unique<GemmOp>(bad_tile), {x, x}, "tile").status().code() ==
+        StatusCode::kInvalidArgument);
+  SoftmaxParams unstable;
+  unstable.numerically_stable = false;
+  CHECK(g.add_node(std::make_unique<SoftmaxOp>(unstable), {x}, "u").status().code() == StatusCode::kUnimplemented);
+  ReduceParams axis0;
+  axis0.axis = 0;
+  CHECK(g.add_node(std::make_unique<ReduceOp>(axis0), {x}, "ax").status().code() == StatusCode::kInvalidArgument);
+}
+
+TEST(op_costs_are_the_ideal_formulas) {
+  GemmParams gp;
+  const GemmOp gemm(gp);
+  const OpCost g = gemm.cost({Shape{8192, 8192}, Shape{8192, 8192}});
+  CHECK(g.flops == 2ull * 8192 * 8192 * 8192);
+  CHECK(g.bytes == 3ull * 8192 * 8192 * 4);
+  const OpCost ba = BiasActOp(BiasActParams{BiasActParams::Act::kGeluTanh}).cost({Shape{16384, 4096}, Shape{4096}});
+  CHECK(ba.bytes == 536887296ull && ba.flops == 10ull * 16384 * 4096);
+  CHECK(BiasActOp(BiasActParams{BiasActParams::Act::kGeluErf}).cost({Shape{2, 2}, Shape{2}}).flops == 4 * 22);
+  CHECK(BiasActOp(BiasActParams{BiasActParams::Act::kNone}).cost({Shape{2, 2}, Shape{2}}).flops == 4);
+  const OpCost rs = ReduceOp(ReduceParams{}).cost({Shape{8192, 8192}});
+  CHECK(rs.bytes == 268468224ull && rs.flops == 8192ull * 8191);
+  ReduceParams mx;
+  mx.kind = ReduceParams::Kind::kMax;
+  CHECK(ReduceOp(mx).cost({Shape{8192, 8192}}).flops == 0);
+  const OpCost sm = SoftmaxOp(SoftmaxParams{}).cost({Shape{32768, 4096}});
+  CHECK(sm.bytes == 1073741824ull && sm.flops == 5ull * 32768 * 4096);
+  // shapes
+  CHECK((*ReduceOp(ReduceParams{}).infer_shapes({Shape{3, 5, 7}}))[0] == (Shape{3, 5}));
+  CHECK((*ReduceOp(ReduceParams{}).infer_shapes({Shape{7}}))[0] == (Shape{1}));
+  // roofline time: a 8192^3 GEMM at 157.3 TFLOP/s vs its bytes at 8 TB/s: compute-bound.
+  const Roofline rl = mi355x_roofline();
+  CHECK(!rl.memory_bound(g.arithmetic_intensity()) && rl.memory_bound(ba.arithmetic_intensity()));
+  CHECK(std::fabs(rl.ridge_point_ai() - 157.3e12 / 8e12) < 1e-9);
+}
+
+// ---------------------------------------------------------------------------
+TEST(schedule_fanout_policies) {
+  Built b = fanout(4, 4, 64, 64);
+  const Roofline rl{1.0, 8000.0};
+  // chain-greedy: every branch continues its own stream -> no events, no waits.
+  auto cg = plan_streams(b.g, SchedulePolicy::kChainGreedy, 4, rl);
+  CHECK(cg.ok());
+  CHECK_EQ(cg->num_streams_used, std::size_t{4});
+  CHECK_EQ(cg->num_events, std::size_t{0});
+  CHECK_EQ(cg->waits_dedup, std::size_t{0});
+  CHECK_OK(verify_plan_ordering(b.g, *cg));
+  // level-parallel: 3 level boundaries x 4 streams x 3 other streams = 36 waits;
+  // every node of levels 0..2 is waited on -> 12 records.
+  auto lp = plan_streams(b.g, SchedulePolicy::kLevelParallel, 4, rl);
+  CHECK(lp.ok());
+  CHECK_EQ(lp->num_events, std::size_t{12});
+  CHECK_EQ(lp->waits_raw, std::size_t{36});
+  CHECK_EQ(lp->waits_dedup, std::size_t{36});
+  CHECK_OK(verify_plan_ordering(b.g, *lp));
+  // sequential: one stream, nothing to record.
+  auto sq = plan_streams(b.g, SchedulePolicy::kSequential, 4, rl);
+  CHECK(sq.ok() && sq->num_streams_used == 1 && sq->num_events == 0);
+  // more streams than nodes in a level: only 4 used.
+  auto cg8 = plan_streams(b.g, SchedulePolicy::kChainGreedy, 8, rl);
+  CHECK(cg8.ok() && cg8->num_streams_used == 4 && cg8->num_streams_requested == 8);
+  CHECK(plan_streams(b.g, SchedulePolicy::kChainGreedy, 0, rl).status().code() == StatusCode::kInvalidArgument);
+}
+
+TEST(schedule_chain_has_no_events) {
+  Built b = chain(16, 32, 32);
+  const Roofline rl{1.0, 8000.0};
+  for (auto p : {SchedulePolicy::kSequential, SchedulePolicy::kLevelParallel, SchedulePolicy::kChainGreedy}) {
+    auto sa = plan_streams(b.g, p, 4, rl);
+    CHECK(sa.ok());
+    // width 1: one stream is enough for every policy, so no cross-stream events.
+    CHECK_EQ(sa->num_streams_used, std::size_t{1});
+    CHECK_EQ(sa->num_events, std::size_t{0});
+  }
+}
+
+TEST(schedule_diamond_and_happens_before) {
+  Built b = diamond(64, 64);
+  auto sa = plan_streams(b.g, SchedulePolicy::kChainGreedy, 2, Roofline{1.0, 8000.0});
+  CHECK(sa.ok());
+  // topo: a(0), l(1), r(2), d(3).  a -> s0; l: one pred (a) not continued -> s0;
+  // r: one pred (a) already continued -> least loaded stream = s1; d: pred l -> s0.
+  CHECK(sa->stream_of[0] == 0 && sa->stream_of[1] == 0 && sa->stream_of[2] == 1 && sa->stream_of[3] == 0);
+  // r waits on a's event: one record, one wait.
+  CHECK_EQ(sa->num_events, std::size_t{1});
+  CHECK_EQ(sa->waits_dedup, std::size_t{1});
+  auto hb = sa->happens_before();
+  CHECK(hb.ok());
+  CHECK(hb->precedes(0, 1) && hb->precedes(0, 2) && hb->precedes(0, 3) && hb->precedes(1, 3));
+  CHECK(hb->concurrent(2, 3) && hb->concurrent(1, 2));
+  CHECK(!hb->precedes(3, 0));
+}
+
+TEST(happens_before_rejects_malformed) {
+  // two nodes sharing an issue index on one stream
+  CHECK(!HappensBefore::build(1, {0, 0}, {0, 0}, {kNoEventId, kNoEventId}, {{}, {}}, {0, 1}).ok());
+  // waiting on an event nobody records
+  CHECK(!HappensBefore::build(2, {0, 1}, {0, 0}, {kNoEventId, kNoEventId}, {{}, {7}}, {0, 1}).ok());
+  // gap in the issue indices
+  CHECK(!HappensBefore::build(1, {0, 0}, {0, 2}, {kNoEventId, kNoEventId}, {{}, {}}, {0, 1}).ok());
+  // stream out of range
+  CHECK(!HappensBefore::build(1, {0, 1}, {0, 0}, {kNoEventId, kNoEventId}, {{}, {}}, {0, 1}).ok());
+  // a well-formed cross-stream edge
+  auto hb = HappensBefore::build(2, {0, 1}, {0, 0}, {0, kNoEventId}, {{}, {0}}, {0, 1});
+  CHECK(hb.ok() && hb->precedes(0, 1) && !hb->precedes(1, 0));
+}
+
+// ---------------------------------------------------------------------------
+TEST(memory_chain16_exact_bytes) {
+  Built b = chain(16, 64, 64);   // every tensor 16 KiB, bias 256 B
+  auto sa = plan_streams(b.g, SchedulePolicy::kSequential, 1, Roofline{1.0, 8000.0});
+  auto hb = sa->happens_before();
+  auto mp = plan_memory(b.g, *sa, *hb, MemoryPolicy::kReuseHappensBefore);
+  CHECK(mp.ok());
+  // x, 16 node outputs (last is the graph output), bias: 17 x 16 KiB + 256 naive.
+  CHECK_EQ(mp->naive_bytes, std::size_t{17 * 16384 + 256});
+  // x + two ping-pong intermediates + the output + the bias.
+  CHECK_EQ(mp->arena_bytes, std::size_t{4 * 16384 + 256});
+  CHECK_EQ(mp->buffers_used, std::size_t{5});
+  CHECK_OK(verify_no_buffer_races(b.g, *sa, *hb, *mp));
+  auto per = plan_memory(b.g, *sa, *hb, MemoryPolicy::kAllocPerTensor);
+  CHECK(per.ok() && per->arena_bytes == per->naive_bytes);
+  for (std::size_t t = 0; t < b.g.num_tensors(); ++t) CHECK(mp->offset_of[t] % kDeviceAlignment == 0);
+}
+
+TEST(memory_unsafe_arm_is_flagged) {
+  // Fan-out on 4 streams: branches run concurrently.  Topological-position reuse
+  // lets a later branch's tensor take an earlier branch's bytes with no ordering
+  // between them: the race verifier must reject that plan, and the
+  // happens-before plan must pass.
+  Built b = fanout(4, 4, 64, 64);
+  auto sa = plan_streams(b.g, SchedulePolicy::kChainGreedy, 4, Roofline{1.0, 8000.0});
+  auto hb = sa->happens_before();
+  auto naive = plan_memory(b.g, *sa, *hb, MemoryPolicy::kReuseTopoNaive);
+  CHECK(naive.ok());
+  CHECK(verify_no_buffer_races(b.g, *sa, *hb, *naive).code() == StatusCode::kInternal);
+  auto safe = plan_memory(b.g, *sa, *hb, MemoryPolicy::kReuseHappensBefore);
+  CHECK(safe.ok());
+  CHECK_OK(verify_no_buffer_races(b.g, *sa, *hb, *safe));
+  auto same = plan_memory(b.g, *sa, *hb, MemoryPolicy::kReuseSameStream);
+  CHECK_OK(verify_no_buffer_races(b.g, *sa, *hb, *same));
+  // Concurrency costs memory: 4 streams need more arena than 1.
+  auto sa1 = plan_streams(b.g, SchedulePolicy::kSequential, 1, Roofline{1.0, 8000.0});
+  auto hb1 = sa1->happens_before();
+  auto one = plan_memory(b.g, *sa1, *hb1, MemoryPolicy::kReuseHappensBefore);
+  CHECK(one->arena_bytes < safe->arena_bytes);
+}
+
+TEST(memory_and_schedule_fuzz_random_dags) {
+  std::mt19937 rng(1234);
+  for (int trial = 0; trial < 60; ++trial) {
+    Graph g;
+    const dim_t n = 32;
+    std::vector<TensorId> pool{*g.add_input(Shape{n, n}, DType::kF32, "x")};
+    const TensorId bi = *g.add_input(Shape{n}, DType::kF32, "b");
+    const int nodes = 4 + static_cast<int>(rng() % 20);
+    for (int i = 0; i < nodes; ++i) {
+      const TensorId src = pool[rng() % pool.size()];
+      const int kind = static_cast<int>(rng() % 3);
+      TensorId out;
+      if (kind == 0) {
+        out = (*g.add_node(bias_act(), {src, bi}, "ba" + std::to_string(i)))[0];
+      } else if (kind == 1) {
+        out = (*g.add_node(std::make_unique<SoftmaxOp>(SoftmaxParams{}), {src}, "sm" + std::to_string(i)))[0];
+      } else {
+        const TensorId other = pool[rng() % pool.size()];
+        GemmParams gp;
+        gp.variant = K::GemmVariant::kMfmaF32;
+        gp.auto_tile = true;
+        out = (*g.add_node(std::make_unique<GemmOp>(gp), {src, other}, "mm" + std::to_string(i)))[0];
+      }
+      pool.push_back(out);
+    }
+    (void)g.mark_output(pool.back());
+    if (rng() % 2) (void)g.mark_output(pool[pool.size() / 2]);
+    CHECK_OK(g.finalize());
+    for (auto sp : {SchedulePolicy::kSequential, SchedulePolicy::kLevelParallel, SchedulePolicy::kChainGreedy}) {
+      for (int streams : {1, 2, 3, 4}) {
+        auto sa = plan_streams(g, sp, streams, Roofline{1.0, 8000.0});
+        if (!sa.ok()) {
+          CHECK(false);
+          continue;
+        }
+        CHECK_OK(verify_plan_ordering(g, *sa));
+        auto hb = sa->happens_before();
+        CHECK(hb.ok());
+        for (auto mpol : {MemoryPolicy::kAllocPerTensor, MemoryPolicy::kReuseSameStream,
+                          MemoryPolicy::kReuseHappensBefore}) {
+          auto mp = plan_memory(g, *sa, *hb, mpol);
+          CHECK(mp.ok());
+          CHECK_OK(verify_no_buffer_races(g, *sa, *hb, *mp));
+          CHECK(mp->arena_bytes <= mp->naive_bytes);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Buddy allocator on host memory with fake streams.
+class HostBuddy : public BuddyAllocator {
+ public:
+  using BuddyAllocator::BuddyAllocator;
+  mutable std::set<rt::StreamHandle> busy;
+  int raw_allocs = 0, raw_frees = 0;
+
+ protected:
+  bool stream_completed(rt::StreamHandle s) const override { return busy.count(s) == 0; }
+  void wait_stream(rt::StreamHandle s) const override { busy.erase(s); }
+  StatusOr<void*> raw_alloc(std::size_t bytes) override {
+    ++raw_allocs;
+    void* p = std::aligned_alloc(256, bytes);
+    if (!p) return OutOfMemoryError("host aligned_alloc failed");
+    return p;
+  }
+  void raw_free(void* p) override {
+    ++raw_frees;
+    std::free(p);
+  }
+};
+
+static rt::StreamHandle fake_stream(std::uintptr_t id) { return reinterpret_cast<rt::StreamHandle>(id * 0x100); }
+
+static BuddyConfig small_cfg(ReusePolicy p) {
+  BuddyConfig c;
+  c.initial_slab_bytes = 1 << 20;
+  c.large_alloc_threshold = 4 << 20;
+  c.reuse_policy = p;
+  return c;
+}
+
+TEST(buddy_sizes_split_merge_validate) {
+  HostBuddy b(small_cfg(ReusePolicy::kCoarseStreamPoll));
+  const auto s1 = fake_stream(1);
+  auto a = b.allocate(1000, s1);
+  CHECK(a.ok() && a->bytes == 1024 && a->requested_bytes == 1000);
+  CHECK(reinterpret_cast<std::uintptr_t>(a->ptr) % 256 == 0);
+  auto c = b.allocate(100, s1);   // rounds up to the 256-byte minimum block
+  CHECK(c.ok() && c->bytes == 256);
+  CHECK_OK(b.validate());
+  CHECK_EQ(b.stats().bytes_in_use, std::size_t{1280});
+  CHECK_EQ(b.raw_allocs, 1);
+  CHECK_OK(b.deallocate(*a, s1));
+  CHECK_OK(b.deallocate(*c, s1));
+  CHECK_OK(b.validate());
+  // After the parked blocks are reclaimed (same stream), the slab merges back to
+  // one 1 MiB block: a 1 MiB request fits without a new slab.
+  auto whole = b.allocate(1 << 20, s1);
+  CHECK(whole.ok() && whole->bytes == (1u << 20));
+  CHECK_EQ(b.raw_allocs, 1);
+  CHECK_OK(b.validate());
+  CHECK(b.stats().largest_free_block == 0);
+}
+
+TEST(buddy_stream_ordered_reuse) {
+  for (ReusePolicy pol : {ReusePolicy::kSameStreamOnly, ReusePolicy::kCoarseStreamPoll}) {
+    HostBuddy b(small_cfg(pol));
+    const auto s1 = fake_stream(1), s2 = fake_stream(2);
+    auto a = b.allocate(64 << 10, s1);
+    void* first = a->ptr;
+    b.busy.insert(s1);                      // s1 still has queued work using the block
+    CHECK_OK(b.deallocate(*a, s1));
+    CHECK_EQ(b.stats().deferred_reuses, std::uint64_t{1});
+    auto on_s1 = b.allocate(64 << 10, s1);  // same stream: safe immediately
+    CHECK(on_s1->ptr == first);
+    CHECK_OK(b.deallocate(*on_s1, s1));
+    auto on_s2 = b.allocate(64 << 10, s2);  // other stream, s1 busy: never the same bytes
+    CHECK(on_s2->ptr != first);
+    CHECK_OK(b.deallocate(*on_s2, s2));
+    b.busy.erase(s1);                       // s1 drains
+    auto later = b.allocate(64 << 10, s2);
+    if (pol == ReusePolicy::kCoarseStreamPoll)
+      CHECK(later->ptr == first);           // the poll sees s1 idle and releases the block
+    else
+      CHECK(later->ptr != first || b.stats().blocking_drains > 0);
+    CHECK_OK(b.validate());
+  }
+}
+
+TEST(buddy_blocking_drain_and_oom) {
+  BuddyConfig cfg = small_cfg(ReusePolicy::kCoarseStreamPoll);
+  cfg.max_total_bytes = 1 << 20;
+  HostBuddy b(cfg);
+  const auto s1 = fake_stream(1), s2 = fake_stream(2);
+  auto a = b.allocate(1 << 20, s1);
+  CHECK(a.ok());
+  b.busy.insert(s1);
+  CHECK_OK(b.deallocate(*a, s1));
+  // s2 needs the whole slab; the only copy is parked behind busy s1, and the cap
+  // forbids a new slab: the allocator must wait for s1 (a counted blocking drain).
+  auto c = b.allocate(1 << 20, s2);
+  CHECK(c.ok() && c->ptr == a->ptr);
+  CHECK_EQ(b.stats().blocking_drains, std::uint64_t{1});
+  // Nothing left and the cap reached: out of memory, counted.
+  auto d = b.allocate(256, s2);
+  CHECK(!d.ok() && d.status().code() == StatusCode::kOutOfMemory);
+  CHECK_EQ(b.stats().oom_events, std::uint64_t{1});
+  CHECK_OK(b.deallocate(*c, s2));
+  CHECK_OK(b.validate());
+}
+
+TEST(buddy_growth_bypass_and_trim) {
+  HostBuddy b(small_cfg(ReusePolicy::kCoarseStreamPoll));
+  const auto s1 = fake_stream(1);
+  auto a = b.allocate(768 << 10, s1);      // 1 MiB block: the whole first slab
+  auto c = b.allocate(512 << 10, s1);      // needs a second slab (growth x2 -> 2 MiB)
+  CHECK(a.ok() && c.ok());
+  CHECK_EQ(b.raw_allocs, 2);
+  CHECK_EQ(b.stats().bytes_reserved, std::size_t{3 << 20});
+  auto big = b.allocate(8 << 20, s1);      // above the 4 MiB threshold: its own hipMalloc
+  CHECK(big.ok() && big->slab_id == kBypassSlabId && big->bytes == std::size_t{8 << 20});
+  CHECK_EQ(b.raw_allocs, 3);
+  CHECK_OK(b.deallocate(*big, s1));
+  CHECK_EQ(b.raw_frees, 1);
+  CHECK_OK(b.deallocate(*c, s1));
+  CHECK_OK(b.trim());                      // the second slab is empty again: released
+  CHECK_EQ(b.raw_frees, 2);
+  CHECK_EQ(b.stats().bytes_reserved, std::size_t{1 << 20});
+  CHECK_OK(b.validate());
+  CHECK_OK(b.deallocate(*a, s1));
+  CHECK(b.deallocate(*a, s1).code() == StatusCode::kInvalidArgument);   // double free
+}
+
+TEST(first_bit_mismatch_helper) {
+  const std::uint32_t x[4] = {1, 2, 3, 4};
+  std::uint32_t y[4] = {1, 2, 3, 4};
+  CHECK_EQ(first_bit_mismatch(x, y, 16), std::size_t{16});
+  y[2] = 7;
+  CHECK_EQ(first_bit_mismatch(x, y, 16), std::size_t{8});
+}
+
+int main(int argc, char** argv) { return check::run_all(argc, argv); }

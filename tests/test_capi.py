@@ -17,10 +17,11 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "mcke_amd.h")
+GRAPH_HEADER = os.path.join(ROOT, "include", "mcke_graph.h")
 
 
-def _declared_functions() -> list[str]:
-    text = open(HEADER).read()
+def _declared_functions(header: str = HEADER) -> list[str]:
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(mcke_[a-z0-9_]+)\s*\(", text)))
 
@@ -43,6 +44,34 @@ def test_library_exports_every_declared_symbol(mcke):
     exported = set(re.findall(r"\sT\s(mcke_\w+)", out))
     assert set(_declared_functions()) <= exported
     assert mcke.lib().mcke_abi_version() == 1
+
+
+def test_host_library_exports_every_graph_symbol(mcke):
+    from mcke_amd import graph
+    L = graph.host_lib()
+    names = _declared_functions(GRAPH_HEADER)
+    assert "mcke_executor_validate_numerics" in names and "mcke_graph_add_gemm" in names
+    for name in names:
+        assert hasattr(L, name), f"{name} declared in mcke_graph.h but not exported"
+    out = subprocess.run(["nm", "-D", "--defined-only", graph.host_library_path()],
+                         capture_output=True, text=True, check=True).stdout
+    assert set(names) <= set(re.findall(r"\sT\s(mcke_\w+)", out))
+
+
+def test_graph_builder_without_gpu(mcke):
+    """Graph construction and shape inference are host-only."""
+    from mcke_amd import graph
+    g, t = graph.mlp_block(64, 32, 128)
+    assert g.shape(t["gemm1"]) == (64, 128) and g.shape(t["y"]) == (64, 32)
+    g2 = graph.Graph()
+    x = g2.add_input((4, 4), "x")
+    b = g2.add_input((5,), "b")
+    import pytest as _pt
+    with _pt.raises(mcke.MckeError) as ei:
+        g2.add_bias_act(x, b, "bad")
+    assert ei.value.status.code == mcke.StatusCode.kInvalidArgument
+    with _pt.raises(mcke.MckeError):
+        g2.add_gemm(x, x, "tiled_no_tile", variant=mcke.GemmVariant.kTiledSmem)
 
 
 def test_enum_values_match_reference(mcke):

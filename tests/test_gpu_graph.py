@@ -1,0 +1,154 @@
+"""GPU tests of the graph layer through its C-ABI (include/mcke_graph.h):
+BASELINE config 5's MLP block and GEMM fan-out at reduced sizes, stage by stage
+against the CPU oracle, the bitwise numerics gate over 3 schedules x 3 memory
+policies, plan statistics and the buddy allocator's reuse.
+
+Stage-wise parity: each node's output is compared with the oracle applied to the
+GPU's own input to that node (read back from a per-tensor arena), so a tolerance
+only has to cover one kernel's rounding, as in the kernel tests."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def G(gpu):
+    from mcke_amd import graph
+    return graph
+
+
+def _mlp_inputs(orc, tokens, d_model, d_ff):
+    return {
+        "x": orc.fill_normal(tokens * d_model, 1, 0.0, 1.0),
+        "W1": orc.fill_normal(d_model * d_ff, 2, 0.0, 0.02),
+        "b1": orc.fill_normal(d_ff, 3, 0.0, 0.01),
+        "W2": orc.fill_normal(d_ff * d_model, 4, 0.0, 0.02),
+        "b2": orc.fill_normal(d_model, 5, 0.0, 0.01),
+    }
+
+
+def test_mlp_block_stagewise_parity(G, orc):
+    T, D, F = 256, 128, 512
+    g, t = G.mlp_block(T, D, F)
+    ex = G.Executor(g, schedule=G.SchedulePolicy.kSequential,
+                    memory=G.MemoryPolicy.kAllocPerTensor, num_streams=1)
+    ex.plan()
+    inp = _mlp_inputs(orc, T, D, F)
+    for k, v in inp.items():
+        ex.set_input(t[k], v)
+    ex.run_sync()
+    g1 = ex.read(t["gemm1"], T * F)
+    h = ex.read(t["h"], T * F)
+    g2 = ex.read(t["gemm2"], T * D)
+    z = ex.read(t["z"], T * D)
+    y = ex.read(t["y"], T * D)
+    # GEMMs: K-scaled tolerances with the inputs' magnitude (amax ~ 4 sigma).
+    w = orc.gemm(inp["x"], inp["W1"], np.zeros(T * F, np.float32), T, F, D)
+    r = orc.compare(g1, w, orc.tol_gemm(D), orc.abs_tol_gemm(D, 4.0 * 0.02 * 4.0))
+    assert r.ok, f"gemm1: {r}"
+    r = orc.compare(h, orc.bias_act(g1, inp["b1"], T, F, 3), 1e-6, 1e-6)
+    assert r.ok, f"bias_gelu: {r}"
+    w = orc.gemm(h, inp["W2"], np.zeros(T * D, np.float32), T, D, F)
+    r = orc.compare(g2, w, orc.tol_gemm(F), orc.abs_tol_gemm(F, 0.1))
+    assert r.ok, f"gemm2: {r}"
+    assert np.array_equal(z, orc.bias_act(g2, inp["b2"], T, D, 0))      # bias add: exact
+    r = orc.compare(y, orc.row_softmax(z, T, D), 1e-5, 1e-6)
+    assert r.ok, f"softmax: {r}"
+    # end to end against the oracle chain from the original inputs
+    r1 = orc.gemm(inp["x"], inp["W1"], np.zeros(T * F, np.float32), T, F, D)
+    r2 = orc.gemm(orc.bias_act(r1, inp["b1"], T, F, 3), inp["W2"], np.zeros(T * D, np.float32),
+                  T, D, F)
+    ref = orc.row_softmax(orc.bias_act(r2, inp["b2"], T, D, 0), T, D)
+    assert np.max(np.abs(y - ref)) < 1e-5
+
+
+@pytest.mark.parametrize("schedule", [0, 1, 2])
+@pytest.mark.parametrize("memory", [0, 2, 3])
+def test_mlp_block_same_bits_under_every_plan(G, orc, schedule, memory):
+    T, D, F = 128, 64, 256
+    inp = _mlp_inputs(orc, T, D, F)
+
+    def run(sched, mem, streams):
+        g, t = G.mlp_block(T, D, F)
+        ex = G.Executor(g, schedule=sched, memory=mem, num_streams=streams, poison_buffers=True)
+        ex.plan()
+        for k, v in inp.items():
+            ex.set_input(t[k], v)
+        ex.run_sync()
+        ex.run_sync()     # second run over a re-poisoned arena
+        out = ex.read(t["y"], T * D)
+        ex.close()
+        return out
+
+    gold = run(0, 0, 1)
+    got = run(schedule, memory, 4)
+    assert np.array_equal(gold.view(np.uint32), got.view(np.uint32))
+
+
+def test_numerics_gate_passes(G, orc):
+    T, D, F = 128, 64, 256
+    g, t = G.mlp_block(T, D, F)
+    ex = G.Executor(g, num_streams=4, validate_numerics=True)
+    ex.plan()
+    for k, v in _mlp_inputs(orc, T, D, F).items():
+        ex.set_input(t[k], v)
+    res = ex.validate_numerics(repeats=3)
+    assert res.passed, res.detail
+    assert res.configs_compared == 9
+
+
+def test_gemm_fanout_streams_and_parity(G, orc):
+    n, B, Dp = 256, 4, 4
+    g, t = G.gemm_fanout(B, Dp, n)
+    ex = G.Executor(g, schedule=G.SchedulePolicy.kChainGreedy,
+                    memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4, profile=True)
+    ex.plan()
+    info = ex.plan_info()
+    assert info["num_nodes"] == 16 and info["num_streams_used"] == 4
+    assert info["num_events"] == 0 and info["waits_dedup"] == 0      # independent chains
+    assert info["forkjoin_events"] == 4 + 2 * 3
+    assert info["total_flops"] == 16 * 2 * n ** 3
+    w = (orc.fill_random(n * n, 7) * 0.0625).astype(np.float32)
+    xs = [orc.fill_random(n * n, 100 + k) for k in range(B)]
+    ex.set_input(t["W"], w)
+    for k in range(B):
+        ex.set_input(t["xs"][k], xs[k])
+    for _ in range(3):
+        ex.run_async()
+    ex.synchronize()
+    for k in range(B):
+        want = xs[k]
+        for _ in range(Dp):
+            want = orc.gemm(want, w, np.zeros(n * n, np.float32), n, n, n)
+        got = ex.read(t["outs"][k], n * n)
+        r = orc.compare(got, want, 1e-4, 1e-5)
+        assert r.ok, f"branch {k}: {r}"
+    tim = ex.timings()
+    assert len(tim) == 16 and all(x["samples"] == 3 and x["median_ms"] > 0 for x in tim)
+    assert {x["stream"] for x in tim} == {0, 1, 2, 3}
+
+
+def test_level_parallel_event_counts(G):
+    g, _ = G.gemm_fanout(4, 4, 64)
+    ex = G.Executor(g, schedule=G.SchedulePolicy.kLevelParallel, num_streams=4)
+    ex.plan()
+    info = ex.plan_info()
+    assert info["num_events"] == 12 and info["waits_dedup"] == 36
+
+
+def test_buddy_allocator_reuses_across_plans(G, orc):
+    g, t = G.mlp_block(128, 64, 256)
+    ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, num_streams=2)
+    ex.plan()
+    first = ex.allocator_stats()
+    ex.plan()                      # re-plan: the old arena returns, the new one reuses it
+    ex.plan()
+    s = ex.allocator_stats()
+    assert s["raw_malloc_calls"] == first["raw_malloc_calls"]
+    assert s["reuse_hits"] >= 2 and s["alloc_calls"] > first["alloc_calls"]
+    info = ex.plan_info()
+    assert info["arena_bytes"] <= info["naive_bytes"]
+    assert s["bytes_in_use"] >= info["arena_bytes"]
