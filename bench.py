@@ -213,6 +213,97 @@ def gemm_sweep(m, stream, iters=10):
     return out
 
 
+def graph_section(m, steps=5, warmup=2):
+    """BASELINE config 5 through the GraphExecutor (buddy allocator, chain-greedy
+    schedule, happens-before arena reuse):
+      * the MLP block X[4096x4096] -> GEMM(W1 4096x16384) -> bias+GELU -> GEMM(W2)
+        -> bias -> softmax, per-node times and roofline fractions;
+      * a 4x4 fan-out of 2048^3 GEMM chains on 4 streams vs the same graph on one
+        stream, with the overlap (sum of node times / wall) and buddy statistics."""
+    from mcke_amd import graph as G
+
+    out = {}
+
+    def timed_runs(ex, n):
+        st = ex.stream()
+        e0, e1 = m.Event(), m.Event()
+        for _ in range(warmup):
+            ex.run_async()
+        ex.synchronize()
+        e0.record(st)
+        for _ in range(n):
+            ex.run_async()
+        e1.record(st)
+        ex.synchronize()
+        return e0.elapsed_ms(e1) / n
+
+    T, D, F = 4096, 4096, 16384
+    log("config 5: MLP block 4096x4096 -> 16384 -> 4096")
+    g, t = G.mlp_block(T, D, F)
+    ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, schedule=G.SchedulePolicy.kChainGreedy,
+                    memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4, profile=True,
+                    profile_slots=warmup + steps)
+    ex.plan()
+    ex.set_input(t["x"], m.fill_normal(T * D, 0x3001, 0.0, 1.0))
+    ex.set_input(t["W1"], m.fill_normal(D * F, 0x3002, 0.0, 0.02))
+    ex.set_input(t["b1"], m.fill_normal(F, 0x3003, 0.0, 0.01))
+    ex.set_input(t["W2"], m.fill_normal(F * D, 0x3004, 0.0, 0.02))
+    ex.set_input(t["b2"], m.fill_normal(D, 0x3005, 0.0, 0.01))
+    wall = timed_runs(ex, steps)
+    info = ex.plan_info()
+    nodes = []
+    for x in ex.timings():
+        is_gemm = x["name"].startswith("gemm")
+        ach = (x["flops"] / (x["median_ms"] * 1e-3) / 1e12) if is_gemm else \
+              (x["bytes"] / (x["median_ms"] * 1e-3) / 1e9)
+        peak = PEAK_FP32_MFMA_TFLOPS if is_gemm else PEAK_HBM_GBS
+        nodes.append({"name": x["name"], "median_ms": round(x["median_ms"], 4),
+                      "achieved": round(ach, 1), "unit": "TFLOP/s" if is_gemm else "GB/s",
+                      "frac": round(ach / peak, 4)})
+    bound_ms = sum(max(x["flops"] / (PEAK_FP32_MFMA_TFLOPS * 1e12), x["bytes"] / (PEAK_HBM_GBS * 1e9))
+                   for x in ex.timings()) * 1e3
+    ex.plan()     # re-plan: the new arena comes from the block the old one returned
+    out["mlp_block"] = {
+        "shape": f"X[{T}x{D}] W1[{D}x{F}] W2[{F}x{D}]", "wall_ms": round(wall, 4),
+        "tflops": round(info["total_flops"] / (wall * 1e-3) / 1e12, 2),
+        "roofline_bound_ms": round(bound_ms, 4), "bound_over_wall": round(bound_ms / wall, 4),
+        "nodes": nodes, "arena_bytes": info["arena_bytes"], "naive_bytes": info["naive_bytes"],
+        "allocator": ex.allocator_stats(),
+    }
+    log(f"config 5 MLP: {wall:.3f} ms/run, {out['mlp_block']['tflops']} TFLOP/s")
+    ex.close()
+
+    n, B, Dp = 2048, 4, 4
+    fan = {}
+    for label, sched, streams in (("sequential", G.SchedulePolicy.kSequential, 1),
+                                  ("chain_greedy_4streams", G.SchedulePolicy.kChainGreedy, 4)):
+        g, t = G.gemm_fanout(B, Dp, n)
+        ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, schedule=sched,
+                        memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=streams,
+                        profile=True, profile_slots=warmup + steps)
+        ex.plan()
+        ex.set_input(t["W"], m.fill_random(n * n, 0x4000, -0.03125, 0.03125))
+        for k in range(B):
+            ex.set_input(t["xs"][k], m.fill_random(n * n, 0x4001 + k))
+        wall = timed_runs(ex, steps)
+        tim = ex.timings()
+        node_sum = sum(x["median_ms"] for x in tim)
+        info = ex.plan_info()
+        ex.plan()     # re-plan: exercises the allocator's reuse of the returned arena
+        fan[label] = {"wall_ms": round(wall, 4), "node_sum_ms": round(node_sum, 4),
+                      "overlap": round(node_sum / wall, 3),
+                      "tflops": round(info["total_flops"] / (wall * 1e-3) / 1e12, 2),
+                      "streams": info["num_streams_used"], "events": info["num_events"],
+                      "waits": info["waits_dedup"], "arena_bytes": info["arena_bytes"],
+                      "allocator": ex.allocator_stats()}
+        log(f"config 5 fan-out {label}: {wall:.3f} ms, overlap {node_sum / wall:.2f}")
+        ex.close()
+    fan["speedup_vs_sequential"] = round(fan["sequential"]["wall_ms"] /
+                                         fan["chain_greedy_4streams"]["wall_ms"], 3)
+    out["fanout4x4_gemm2048"] = fan
+    return out
+
+
 def cpu_baseline(m, gemm_bufs, seconds_target=12.0):
     """The CPU reference GEMM (reference tests/reference.hpp:199-211: i-j-p loops,
     double accumulation, one thread) on a row slab of the same 8192^3 problem,
@@ -269,6 +360,7 @@ def main(argv=None) -> int:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-sweep", action="store_true", help="skip the GEMM size sweep")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--no-graph", action="store_true", help="skip the config-5 graph section")
     p.add_argument("--only", default=None,
                    help="comma-separated op-name prefixes to run (profiling); enables "
                         "the copy_256mib calibration op")
@@ -296,6 +388,7 @@ def main(argv=None) -> int:
             f"({100 * s['frac']:.1f}% of {s['peak']})")
 
     sweep = [] if (args.no_sweep or only is not None) else gemm_sweep(m, stream)
+    graph_res = None if (args.no_graph or only is not None) else graph_section(m)
     gemm = summaries[0]
     cpu = None
     if not args.no_cpu and gemm_bufs[0] is not None:
@@ -331,6 +424,7 @@ def main(argv=None) -> int:
         "cpu_baseline": cpu,
         "ops": summaries,
         "gemm_sweep": sweep,
+        "graph": graph_res,
     }
     print(json.dumps(line), flush=True)
     del keep

@@ -29,12 +29,14 @@
 
 namespace mcke {
 
+// Defaults sized for a 288 GB MI355X: 1 GiB first slab, doubling growth, and only
+// requests above 4 GiB bypass the slabs.
 struct BuddyConfig {
-  std::size_t initial_slab_bytes = std::size_t{256} << 20;
+  std::size_t initial_slab_bytes = std::size_t{1} << 30;
   std::size_t max_total_bytes = 0;   // 0 = unlimited
   std::size_t min_block_bytes = kMinBlockBytes;
   double growth_factor = 2.0;
-  std::size_t large_alloc_threshold = std::size_t{64} << 20;
+  std::size_t large_alloc_threshold = std::size_t{4} << 30;
   ReusePolicy reuse_policy = ReusePolicy::kCoarseStreamPoll;
 };
 
