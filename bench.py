@@ -1,9 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MCKE kernel layer on one MI355X.
 
-One *step* runs every hot-path kernel once at its BASELINE.json shape, back to back
-on one stream (so each kernel starts with caches holding the previous kernel's
-data, not its own):
+One *step* runs every hot-path kernel once at its BASELINE.json shape:
 
   gemm      fp32 C = A B, M = N = K = 8192, MFMA variant        (the headline)
   reduce    row sum and row max of X[8192 x 8192]
@@ -12,9 +10,20 @@ data, not its own):
   bias_gelu GELU_tanh(X + b) for X[16384 x 4096] and X[4096 x 1024]
 
 Inputs are generated on the host from seeds and are resident in HBM before the
-timed region.  W untimed steps, then exactly K timed steps bracketed by device
-synchronisation and HIP events; each launch is also bracketed by its own event
-pair on the same stream, which gives every kernel's average launch duration.
+timed region.  Every memory-bound kernel rotates over enough copies of its
+buffers that one rotation moves >= 768 MiB, three times the 256 MB Infinity
+Cache, so each launch reads its input from HBM, not from the cache.
+
+Timing: W untimed steps, then exactly K timed steps bracketed by device
+synchronisation and a pair of HIP events.  Inside the timed region the K launches
+of each kernel run back to back on one stream between their own event pair, so a
+kernel's average launch duration is (that pair's elapsed time) / K: dispatch gaps
+are included, per-launch event overhead is not.  After the timed region a
+diagnostic pass brackets single launches with their own events for median/min.
+
+Also measured in the same run: the denominators (fp32 MFMA peak sustained for
+about the GEMM's duration, a STREAM triad), the GEMM size sweep, the config-5
+graph section and the CPU baseline.
 
 Printed: one JSON line (rank 0, N = 1).  `value` is the GEMM's TFLOP/s; `ops` lists
 every kernel with its roofline fraction; `roofline` is the GEMM's; `cpu_baseline`
@@ -24,7 +33,9 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
+import re
 import sys
 import time
 
@@ -37,6 +48,8 @@ from __graft_entry__ import load_package  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, AMD published
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix, AMD published
+ROTATION_BYTES = 768 << 20     # bytes one rotation of a memory-bound op's buffers moves
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bench_step_hbm_traffic.md")
 
 METRIC = "fp32 GEMM TFLOP/s + reduce/softmax/bias-GELU HBM GB/s, % of roofline"
 
@@ -45,34 +58,64 @@ def log(msg: str) -> None:
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
+def profiled_traffic() -> dict[str, int]:
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (lines `traffic <op> <bytes>`), keyed by op name; {} if absent."""
+    out = {}
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                mt = re.match(r"^traffic\s+(\S+)\s+(\d+)\s*$", line)
+                if mt:
+                    out[mt.group(1)] = int(mt.group(2))
+    except OSError:
+        pass
+    return out
+
+
 class Op:
-    """One kernel launch of the step, with its algorithmic work per launch."""
+    """One kernel of the step: `launch(i)` runs it on buffer set i % sets; `work`
+    is its algorithmic bytes (hbm) or flops (mfma) per launch."""
 
-    def __init__(self, name, launch, bound, work, unit, shape):
+    def __init__(self, name, launch, bound, work, unit, shape, sets=1):
         self.name, self.launch, self.bound = name, launch, bound
-        self.work, self.unit, self.shape = work, unit, shape   # bytes or flops per launch
-        self.times_ms: list[float] = []
+        self.work, self.unit, self.shape, self.sets = work, unit, shape, sets
+        self.total_ms = 0.0
+        self.launches = 0
+        self.single_ms: list[float] = []
 
-    def summary(self):
-        t = np.array(self.times_ms, dtype=np.float64)
-        avg = float(t.mean())
+    def summary(self, measured_peak=None, traffic=None):
+        avg = self.total_ms / self.launches
         if self.bound == "mfma":
             achieved = self.work / (avg * 1e-3) / 1e12
             peak, unit = PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
         else:
             achieved = self.work / (avg * 1e-3) / 1e9
             peak, unit = PEAK_HBM_GBS, "GB/s"
-        return {
+        t = np.array(self.single_ms or [avg], dtype=np.float64)
+        out = {
             "name": self.name, "shape": self.shape, "bound": self.bound,
-            "avg_ms": round(avg, 5), "median_ms": round(float(np.median(t)), 5),
-            "min_ms": round(float(t.min()), 5), "achieved": round(achieved, 2), "unit": unit,
-            "peak": peak, "frac": round(achieved / peak, 4),
+            "avg_ms": round(avg, 5), "launches": self.launches, "buffer_sets": self.sets,
+            "single_launch_median_ms": round(float(np.median(t)), 5),
+            "single_launch_min_ms": round(float(t.min()), 5),
+            "achieved": round(achieved, 2), "unit": unit, "peak": peak,
+            "frac": round(achieved / peak, 4),
             "algorithmic_" + ("flops" if self.bound == "mfma" else "bytes"): self.work,
         }
+        if measured_peak:
+            out["measured_peak"] = round(measured_peak, 2)
+            out["frac_of_measured"] = round(achieved / measured_peak, 4)
+        if traffic is not None:
+            out["hbm_traffic_bytes"] = traffic
+        return out
+
+
+def rotation_sets(bytes_per_launch: int) -> int:
+    return max(1, min(32, math.ceil(ROTATION_BYTES / bytes_per_launch)))
 
 
 def build_ops(m, stream, only=None):
-    """The step's launches; `only` (a set of op-name prefixes) restricts the set,
+    """The step's kernels; `only` (a set of op-name prefixes) restricts the set,
     and also enables the calibration op `copy_256mib` (a plain 256 MiB copy)."""
     D = m.DeviceBuffer
     ops, keep = [], []
@@ -85,7 +128,18 @@ def build_ops(m, stream, only=None):
         if not status.ok():
             raise RuntimeError(str(status))
 
+    def copies(arr, sets):
+        bufs = [D.from_array(arr) for _ in range(sets)]
+        keep.extend(bufs)
+        return bufs
+
+    def outputs(nbytes, sets):
+        bufs = [D(nbytes) for _ in range(sets)]
+        keep.extend(bufs)
+        return bufs
+
     # --- GEMM 8192^3 (BASELINE configs[0] at its largest sweep size) ---------
+    # Compute-bound: one buffer set (A and B are re-read from L2/MALL tiles anyway).
     n = 8192
     a = b = c = None
     if want("gemm_mfma_f32"):
@@ -95,7 +149,7 @@ def build_ops(m, stream, only=None):
         c = D.zeros(n * n)
         tile = m.gemm_mfma_default_tile(n, n, n)
         keep += [a, b, c]
-        ops.append(Op("gemm_mfma_f32", lambda: ck(m.launch_gemm_f32(
+        ops.append(Op("gemm_mfma_f32", lambda i: ck(m.launch_gemm_f32(
             a, b, c, n, n, n, 1.0, 0.0, m.GemmVariant.kMfmaF32, tile, st)),
             "mfma", 2 * n * n * n, "flop", f"{n}x{n}x{n} tile {tile.astuple()}"))
 
@@ -103,25 +157,27 @@ def build_ops(m, stream, only=None):
     R = C_ = 8192
     if want("row_sum") or want("row_max"):
         log("generating reduce input (8192^2 N(0,1))")
-        xr = D.from_array(m.fill_normal(R * C_, 0x5EED12345))
-        outr = D(R * 4)
-        keep += [xr, outr]
         red_bytes = (R * C_ + R) * 4
+        sets = rotation_sets(red_bytes)
+        xr = copies(m.fill_normal(R * C_, 0x5EED12345), sets)
+        outr = outputs(R * 4, sets)
         for kind, nm in ((m.ReduceKind.kSum, "row_sum"), (m.ReduceKind.kMax, "row_max")):
             if want(nm):
-                ops.append(Op(nm, (lambda kind=kind: ck(m.launch_row_reduce_f32(
-                    xr, outr, R, C_, kind, m.ReduceVariant.kWarpShuffle, st))),
-                    "hbm", red_bytes, "byte", f"{R}x{C_}"))
+                ops.append(Op(nm, (lambda i, kind=kind, s=sets: ck(m.launch_row_reduce_f32(
+                    xr[i % s], outr[i % s], R, C_, kind, m.ReduceVariant.kWarpShuffle, st))),
+                    "hbm", red_bytes, "byte", f"{R}x{C_}", sets))
     N26 = 1 << 26
     if want("full_sum"):
         log("generating full-sum input (2^26 U[0,1))")
-        xs = D.from_array(m.fill_random(N26, 0xF011, 0.0, 1.0))
+        fs_bytes = (N26 + 1) * 4
+        sets = rotation_sets(fs_bytes)
+        xs = copies(m.fill_random(N26, 0xF011, 0.0, 1.0), sets)
         wsb = m.row_reduce_workspace_bytes(1, N26, m.ReduceVariant.kTwoPass)
         ws, outs = D(wsb), D(4)
-        keep += [xs, ws, outs]
-        ops.append(Op("full_sum", lambda: ck(m.launch_row_reduce_f32(
-            xs, outs, 1, N26, m.ReduceKind.kSum, m.ReduceVariant.kTwoPass, ws, wsb, st)),
-            "hbm", (N26 + 1) * 4, "byte", "1x2^26"))
+        keep += [ws, outs]
+        ops.append(Op("full_sum", lambda i, s=sets: ck(m.launch_row_reduce_f32(
+            xs[i % s], outs, 1, N26, m.ReduceKind.kSum, m.ReduceVariant.kTwoPass, ws, wsb, st)),
+            "hbm", fs_bytes, "byte", "1x2^26", sets))
 
     # --- softmax -----------------------------------------------
     rows = 32768
@@ -133,58 +189,123 @@ def build_ops(m, stream, only=None):
         rng = np.random.default_rng(cols)
         spike_rows = rng.choice(rows, rows // 100, replace=False)
         x[spike_rows * cols + rng.integers(0, cols, spike_rows.size)] += 30.0
-        dx, dy = D.from_array(x), D(rows * cols * 4)
-        keep += [dx, dy]
-        ops.append(Op(f"softmax_c{cols}", (lambda dx=dx, dy=dy, cols=cols: ck(
-            m.launch_row_softmax_f32(dx, dy, rows, cols, m.SoftmaxVariant.kOnlineOnePass, st))),
-            "hbm", 2 * rows * cols * 4, "byte", f"{rows}x{cols}"))
+        sm_bytes = 2 * rows * cols * 4
+        sets = rotation_sets(sm_bytes)
+        dx, dy = copies(x, sets), outputs(rows * cols * 4, sets)
+        ops.append(Op(f"softmax_c{cols}", (lambda i, dx=dx, dy=dy, cols=cols, s=sets: ck(
+            m.launch_row_softmax_f32(dx[i % s], dy[i % s], rows, cols,
+                                     m.SoftmaxVariant.kOnlineOnePass, st))),
+            "hbm", sm_bytes, "byte", f"{rows}x{cols}", sets))
 
     # --- bias + GELU(tanh) -------------------------------------
     for (br, bc) in ((16384, 4096), (4096, 1024)):
         if not want(f"bias_gelu_{br}x{bc}"):
             continue
         log(f"generating bias+GELU input ({br}x{bc})")
-        dx = D.from_array(m.fill_normal(br * bc, 0xB1A5AC7 + br))
-        db = D.from_array(m.fill_random(bc, 0xB1A5B1A5, -0.5, 0.5))
-        dy = D(br * bc * 4)
-        keep += [dx, db, dy]
-        ops.append(Op(f"bias_gelu_{br}x{bc}", (lambda dx=dx, db=db, dy=dy, br=br, bc=bc: ck(
-            m.launch_bias_act_f32(dx, db, dy, br, bc, m.Activation.kGeluTanh, 4, st))),
-            "hbm", (2 * br * bc + bc) * 4, "byte", f"{br}x{bc}"))
+        bg_bytes = (2 * br * bc + bc) * 4
+        sets = rotation_sets(bg_bytes)
+        dx = copies(m.fill_normal(br * bc, 0xB1A5AC7 + br), sets)
+        db = copies(m.fill_random(bc, 0xB1A5B1A5, -0.5, 0.5), sets)
+        dy = outputs(br * bc * 4, sets)
+        ops.append(Op(f"bias_gelu_{br}x{bc}", (lambda i, dx=dx, db=db, dy=dy, br=br, bc=bc, s=sets: ck(
+            m.launch_bias_act_f32(dx[i % s], db[i % s], dy[i % s], br, bc,
+                                  m.Activation.kGeluTanh, 4, st))),
+            "hbm", bg_bytes, "byte", f"{br}x{bc}", sets))
 
     # --- calibration: a plain copy of known size (only when asked for) -------
     if only is not None and want("copy_256mib"):
         nc = 1 << 26
-        dx, dy = D.from_array(np.ones(nc, np.float32)), D(nc * 4)
-        keep += [dx, dy]
-        ops.append(Op("copy_256mib", lambda: ck(m.launch_activation_f32(
-            dx, dy, nc, m.Activation.kNone, 4, st)), "hbm", 2 * nc * 4, "byte", "2^26 floats"))
+        sets = rotation_sets(2 * nc * 4)
+        dx, dy = copies(np.ones(nc, np.float32), sets), outputs(nc * 4, sets)
+        ops.append(Op("copy_256mib", lambda i, s=sets: ck(m.launch_activation_f32(
+            dx[i % s], dy[i % s], nc, m.Activation.kNone, 4, st)), "hbm", 2 * nc * 4, "byte",
+            "2^26 floats", sets))
     m.device_synchronize()
     return ops, keep, (a, b, c, n)
 
 
 def run_steps(m, stream, ops, steps, record):
-    """Enqueue `steps` steps back to back (no host synchronisation inside), each
-    launch bracketed by its own event pair when `record`."""
-    pairs = [[(m.Event(), m.Event()) for _ in ops] for _ in range(steps)] if record else None
+    """`steps` steps: for each op, `steps` launches back to back on rotating
+    buffers, between the op's own event pair when `record`.  Returns the elapsed
+    time of the whole region (ms), bracketed by synchronisation and events."""
     t0, t1 = m.Event(), m.Event()
+    marks = [(m.Event(), m.Event()) for _ in ops] if record else None
     stream.synchronize()
     t0.record(stream)
-    for s in range(steps):
-        for i, op in enumerate(ops):
-            if record:
-                pairs[s][i][0].record(stream)
-            op.launch()
-            if record:
-                pairs[s][i][1].record(stream)
+    for i, op in enumerate(ops):
+        if record:
+            marks[i][0].record(stream)
+        for s in range(steps):
+            op.launch(s)
+        if record:
+            marks[i][1].record(stream)
     t1.record(stream)
     stream.synchronize()
     if record:
-        for s in range(steps):
-            for i, op in enumerate(ops):
-                e0, e1 = pairs[s][i]
-                op.times_ms.append(e0.elapsed_ms(e1))
+        for i, op in enumerate(ops):
+            op.total_ms += marks[i][0].elapsed_ms(marks[i][1])
+            op.launches += steps
     return t0.elapsed_ms(t1)
+
+
+def single_launches(m, stream, ops, count):
+    """Diagnostic: `count` launches of each op, each between its own event pair."""
+    for op in ops:
+        pairs = [(m.Event(), m.Event()) for _ in range(count)]
+        for s in range(count):
+            pairs[s][0].record(stream)
+            op.launch(s)
+            pairs[s][1].record(stream)
+        stream.synchronize()
+        op.single_ms = [e0.elapsed_ms(e1) for e0, e1 in pairs]
+
+
+def measured_peaks(m, stream, gemm_ms, iters=5):
+    """The measured denominators: fp32 MFMA throughput sustained for about
+    `gemm_ms` per launch (4 waves per SIMD), and a STREAM triad over 3 x 256 MiB
+    arrays rotating over two sets."""
+    D = m.DeviceBuffer
+    out = {}
+    info = m.query_device(0)
+    blocks = info.sm_count * 4
+    seed = D.from_array((np.arange(256, dtype=np.float32) % 7 - 3) * 0.25)
+    sink = D(blocks * 256 * 4)
+    per_iter = m.mfma_peak_flops(blocks, 1)
+    mfma_iters = max(1, int(gemm_ms * 1e-3 * PEAK_FP32_MFMA_TFLOPS * 1e12 / per_iter))
+    ck = lambda st: st.throw_if_error()   # noqa: E731
+    ck(m.launch_mfma_peak_f32(seed, sink, blocks, mfma_iters, stream))
+    e0, e1 = m.Event(), m.Event()
+    e0.record(stream)
+    for _ in range(iters):
+        m.launch_mfma_peak_f32(seed, sink, blocks, mfma_iters, stream)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1) / iters
+    out["mfma_f32_tflops"] = round(m.mfma_peak_flops(blocks, mfma_iters) / (ms * 1e-3) / 1e12, 2)
+    out["mfma_f32_launch_ms"] = round(ms, 4)
+    nt = 1 << 26
+    arrs = [(D.from_array(np.full(nt, 1.0, np.float32)), D.from_array(np.full(nt, 2.0, np.float32)),
+             D(nt * 4)) for _ in range(2)]
+    for s in range(2):
+        ck(m.launch_stream_triad_f32(arrs[s][0], arrs[s][1], arrs[s][2], 3.0, nt, stream))
+    reps = 20
+    e0.record(stream)
+    for s in range(reps):
+        bb, cc, aa = arrs[s % 2]
+        m.launch_stream_triad_f32(bb, cc, aa, 3.0, nt, stream)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    out["stream_triad_gb_s"] = round(3 * nt * 4 / (ms * 1e-3) / 1e9, 1)
+    got = arrs[1][2].download(16)
+    if not np.all(got == 7.0):
+        raise RuntimeError(f"stream triad produced {got[:4]}, expected 7.0")
+    out["note"] = ("mfma: blocks = 4 x CUs, 4 waves each, 4 chains of v_mfma_f32_32x32x2_f32, "
+                   f"{mfma_iters} iterations (~GEMM launch length); triad: a = 3c + b over "
+                   "3 x 256 MiB, two rotating sets")
+    log(f"measured peaks: MFMA fp32 {out['mfma_f32_tflops']} TFLOP/s, "
+        f"triad {out['stream_triad_gb_s']} GB/s")
+    return out
 
 
 def gemm_sweep(m, stream, iters=10):
@@ -361,6 +482,7 @@ def main(argv=None) -> int:
     p.add_argument("--no-sweep", action="store_true", help="skip the GEMM size sweep")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-graph", action="store_true", help="skip the config-5 graph section")
+    p.add_argument("--no-peaks", action="store_true", help="skip the measured-peak microbenches")
     p.add_argument("--only", default=None,
                    help="comma-separated op-name prefixes to run (profiling); enables "
                         "the copy_256mib calibration op")
@@ -370,6 +492,9 @@ def main(argv=None) -> int:
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
               "kernel layer has no multi-GPU path to measure.", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: need --steps >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
 
     m = load_package()
@@ -382,7 +507,20 @@ def main(argv=None) -> int:
     run_steps(m, stream, ops, args.warmup, record=False)
     log(f"timed: {args.steps} steps")
     total_ms = run_steps(m, stream, ops, args.steps, record=True)
-    summaries = [op.summary() for op in ops]
+    log("timed region done; single-launch diagnostic pass")
+    single_launches(m, stream, ops, min(args.steps, 10))
+
+    peaks = None
+    if not args.no_peaks and only is None:
+        gemm_ms = ops[0].total_ms / ops[0].launches if ops[0].bound == "mfma" else 8.0
+        peaks = measured_peaks(m, stream, gemm_ms)
+    traffic = profiled_traffic()
+    summaries = []
+    for op in ops:
+        mp = None
+        if peaks:
+            mp = peaks["mfma_f32_tflops"] if op.bound == "mfma" else peaks["stream_triad_gb_s"]
+        summaries.append(op.summary(mp, traffic.get(op.name)))
     for s in summaries:
         log(f"{s['name']:>20s} {s['avg_ms']:.4f} ms  {s['achieved']:.1f} {s['unit']}  "
             f"({100 * s['frac']:.1f}% of {s['peak']})")
@@ -419,8 +557,10 @@ def main(argv=None) -> int:
         },
         "roofline": {
             "bound": gemm["bound"], "achieved": gemm["achieved"], "peak": gemm["peak"],
-            "unit": gemm["unit"], "frac": gemm["frac"], "traffic": None,
+            "unit": gemm["unit"], "frac": gemm["frac"],
+            "traffic": traffic.get(gemm["name"]),
         },
+        "measured_peaks": peaks,
         "cpu_baseline": cpu,
         "ops": summaries,
         "gemm_sweep": sweep,

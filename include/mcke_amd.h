@@ -209,6 +209,21 @@ int mcke_rt_memset_async(void* dst, int value, size_t bytes, void* stream);
  * executor to poison its arena between runs. */
 int mcke_fill_u32_async(void* dst, uint32_t value, size_t count, void* stream);
 
+/* ---- measured denominators (reference bench/fma_peak.cu, bench/stream_triad.cu) ----
+ * mfma_peak: `blocks` workgroups of 256 lanes; every wave issues `iters` x 4
+ * independent v_mfma_f32_32x32x2_f32 and no other memory traffic than reading
+ * seed[0..255] and writing out[blocks*256].  mcke_mfma_peak_flops() gives the
+ * flops of one launch (blocks * 4 waves * iters * 4 * 4096); 0 for bad arguments.
+ * The reference measures the vector FMA pipe; the GEMM here runs on the matrix
+ * cores, whose fp32 pipe this measures instead.
+ * stream_triad: a[i] = scalar * c[i] + b[i] for i < n (12 bytes per element);
+ * 16-byte aligned a, b, c; a must not alias b or c. */
+uint64_t mcke_mfma_peak_flops(int64_t blocks, int64_t iters);
+int mcke_launch_mfma_peak_f32(const float* seed, float* out, int64_t blocks, int64_t iters,
+                              void* stream);
+int mcke_launch_stream_triad_f32(const float* b, const float* c, float* a, float scalar, int64_t n,
+                                 void* stream);
+
 /* ---- host data generators (bench / test inputs) ----------------------------
  * The same map as the reference's fill_random (tests/reference.hpp:101-109):
  * std::mt19937_64(seed), u = (e >> 40) / 2^24, x = lo + u*(hi - lo).  The normal

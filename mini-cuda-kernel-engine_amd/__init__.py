@@ -201,6 +201,9 @@ def lib() -> C.CDLL:
         "mcke_rt_host_free": (C.c_int, [_VP]),
         "mcke_rt_memcpy_async": (C.c_int, [_VP, _VP, C.c_size_t, C.c_int, _VP]),
         "mcke_rt_memset_async": (C.c_int, [_VP, C.c_int, C.c_size_t, _VP]),
+        "mcke_mfma_peak_flops": (C.c_uint64, [_I64, _I64]),
+        "mcke_launch_mfma_peak_f32": (C.c_int, [_VP, _VP, _I64, _I64, _VP]),
+        "mcke_launch_stream_triad_f32": (C.c_int, [_VP, _VP, _VP, C.c_float, _I64, _VP]),
         "mcke_fill_random_f32": (None, [_VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
         "mcke_fill_normal_f32": (None, [_VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
     }
@@ -491,6 +494,22 @@ def gemm_mfma_default_tile(m: int, n: int, k: int) -> GemmTile:
     t = GemmTile()
     _check(lib().mcke_gemm_mfma_default_tile(m, n, k, C.byref(t)))
     return t
+
+
+# ---------------------------------------------------------------------------
+# Measured denominators (bench/fma_peak.cu, bench/stream_triad.cu counterparts)
+# ---------------------------------------------------------------------------
+def mfma_peak_flops(blocks: int, iters: int) -> int:
+    return int(lib().mcke_mfma_peak_flops(blocks, iters))
+
+
+def launch_mfma_peak_f32(seed, out, blocks: int, iters: int, stream=None) -> Status:
+    return _st(lib().mcke_launch_mfma_peak_f32(_ptr(seed), _ptr(out), blocks, iters, _sh(stream)))
+
+
+def launch_stream_triad_f32(b, c, a, scalar: float, n: int, stream=None) -> Status:
+    return _st(lib().mcke_launch_stream_triad_f32(_ptr(b), _ptr(c), _ptr(a), scalar, n,
+                                                  _sh(stream)))
 
 
 MFMA_TILES = (
