@@ -267,7 +267,10 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     D = m.DeviceBuffer
     out = {}
     info = m.query_device(0)
-    blocks = info.sm_count * 4
+    # Two waves per SIMD (2 workgroups of 4 waves per CU): 1, 2 and 8 waves per
+    # SIMD all sustain the same rate; 4 workgroups per CU (1024 on 256 CUs)
+    # measured ~20% lower, from uneven placement of workgroups on CUs.
+    blocks = info.sm_count * 2
     seed = D.from_array((np.arange(256, dtype=np.float32) % 7 - 3) * 0.25)
     sink = D(blocks * 256 * 4)
     per_iter = m.mfma_peak_flops(blocks, 1)
@@ -300,7 +303,7 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     got = arrs[1][2].download(16)
     if not np.all(got == 7.0):
         raise RuntimeError(f"stream triad produced {got[:4]}, expected 7.0")
-    out["note"] = ("mfma: blocks = 4 x CUs, 4 waves each, 4 chains of v_mfma_f32_32x32x2_f32, "
+    out["note"] = ("mfma: blocks = 2 x CUs, 4 waves each, 4 chains of v_mfma_f32_32x32x2_f32, "
                    f"{mfma_iters} iterations (~GEMM launch length); triad: a = 3c + b over "
                    "3 x 256 MiB, two rotating sets")
     log(f"measured peaks: MFMA fp32 {out['mfma_f32_tflops']} TFLOP/s, "

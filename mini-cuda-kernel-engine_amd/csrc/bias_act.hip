@@ -7,9 +7,14 @@
 //     VW consecutive columns, so a wave issues 64 x VW x 4 contiguous bytes
 //     (1 KiB at VW = 4: 16-byte global_load_dwordx4 per lane);
 //   * the bias vector for those columns is loaded once and kept in registers;
-//   * one workgroup row per matrix row, so every lane has one 16-byte load in
-//     flight and the whole launch is resident at once (rows beyond the grid's
-//     65535 limit are walked with a stride of gridDim.y, four per iteration);
+//   * large launches: one workgroup row per matrix row, so every lane has one
+//     16-byte load in flight and the hardware streams workgroups through the CUs
+//     (rows beyond the grid's 65535 limit are walked with a stride of gridDim.y,
+//     four per iteration);
+//   * small launches (at most two rounds of resident workgroups at one row each):
+//     each workgroup owns kChunkRows adjacent rows of its column strip and issues
+//     all their loads before any store, so the launch is one round of
+//     long-latency loads instead of two;
 //   * x and y are streamed with non-temporal loads/stores.
 #include <hip/hip_runtime.h>
 
@@ -23,6 +28,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowUnroll = 4;
+constexpr int kChunkRows = 8;
+// At or below this many one-row workgroups a launch takes the chunked kernel.
+constexpr int64_t kChunkMaxBlocks = 4096;
 
 template <int VW, int ACT>
 __global__ __launch_bounds__(kThreads) void bias_act_kernel(const float* __restrict__ x,
@@ -55,6 +63,42 @@ __global__ __launch_bounds__(kThreads) void bias_act_kernel(const float* __restr
           for (int i = 0; i < VW; ++i) o[i] = act_xb<ACT>(a[u][i], bv[i]);
         }
         st_stream(yv + rr * cols_v, o);
+      }
+    }
+  }
+}
+
+// Small launches: workgroup row blockIdx.y owns R adjacent matrix rows at a time
+// (chunks strided by gridDim.y), all R loads issued before the first store.
+template <int VW, int ACT, int R>
+__global__ __launch_bounds__(kThreads) void bias_act_chunk_kernel(const float* __restrict__ x,
+                                                                  const float* __restrict__ bias,
+                                                                  float* __restrict__ y,
+                                                                  int64_t rows, int64_t cols_v) {
+  using V = Vec<VW>;
+  const int64_t cv = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (cv >= cols_v) return;
+  const V bv = reinterpret_cast<const V*>(bias)[cv];
+  const V* __restrict__ xv = reinterpret_cast<const V*>(x) + cv;
+  V* __restrict__ yv = reinterpret_cast<V*>(y) + cv;
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * R; r0 < rows;
+       r0 += static_cast<int64_t>(gridDim.y) * R) {
+    V a[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      if (r0 + u < rows) a[u] = ld_stream(xv + (r0 + u) * cols_v);
+    }
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      if (r0 + u < rows) {
+        V o;
+        if constexpr (VW == 1) {
+          o = act_xb<ACT>(a[u], bv);
+        } else {
+#pragma unroll
+          for (int i = 0; i < VW; ++i) o[i] = act_xb<ACT>(a[u][i], bv[i]);
+        }
+        st_stream(yv + (r0 + u) * cols_v, o);
       }
     }
   }
@@ -123,9 +167,9 @@ int validate_2d(const char* who, const float* x, const float* y, int64_t rows, i
 // with a smaller grid measured 3-10% slower).  Capped at the hardware's 65535,
 // beyond which lanes walk the remaining rows kRowUnroll at a time, and at the
 // caller's max_row_blocks.
-dim3 grid_2d(int64_t rows, int64_t cols_v, int max_row_blocks) {
+dim3 grid_2d(int64_t rows, int64_t cols_v, int max_row_blocks, int rows_per_block = 1) {
   const int64_t gx = (cols_v + kThreads - 1) / kThreads;
-  int64_t gy = rows;
+  int64_t gy = (rows + rows_per_block - 1) / rows_per_block;
   if (gy > 65535) gy = 65535;
   if (max_row_blocks > 0 && gy > max_row_blocks) gy = max_row_blocks;
   if (gy < 1) gy = 1;
@@ -136,6 +180,21 @@ template <int VW>
 int launch_fused_vw(const float* x, const float* bias, float* y, int64_t rows, int64_t cols,
                     int act, hipStream_t s, int max_row_blocks) {
   const int64_t cols_v = cols / VW;
+  const int64_t gx = (cols_v + kThreads - 1) / kThreads;
+  if (gx * rows <= kChunkMaxBlocks) {
+    const dim3 grid = grid_2d(rows, cols_v, max_row_blocks, kChunkRows);
+#define MCKE_CHUNK(A) bias_act_chunk_kernel<VW, A, kChunkRows><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v)
+    switch (act) {
+      case kActNone: MCKE_CHUNK(kActNone); break;
+      case kActRelu: MCKE_CHUNK(kActRelu); break;
+      case kActGeluErf: MCKE_CHUNK(kActGeluErf); break;
+      case kActGeluTanh: MCKE_CHUNK(kActGeluTanh); break;
+      default: return invalid("launch_bias_act_f32: unknown activation " + std::to_string(act));
+    }
+#undef MCKE_CHUNK
+    MCKE_LAUNCH_CHECK("bias_act_chunk_kernel");
+    return ok();
+  }
   const dim3 grid = grid_2d(rows, cols_v, max_row_blocks);
   switch (act) {
     case kActNone: bias_act_kernel<VW, kActNone><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v); break;

@@ -52,23 +52,14 @@ template <int WIDTH = 64> __device__ __forceinline__ float wave_max(float v) {
 // ---------------------------------------------------------------------------
 // Activations (reference tests/reference.hpp:116-136 and bias_act.cu:95-117).
 //
-// Each takes x and the bias separately so that v = x + b is carried exactly as
-// (vh, vl) with vh = fl(x + b) (Knuth's TwoSum), matching the reference's double
-// sum, and the GELUs are evaluated in forms that keep the absolute error near
-// half an ulp of the result:
-//
-//   GELU_tanh(v) = 0.5 v (1 + tanh(z)),  z = sqrt(2/pi) (v + 0.044715 v^3)
-//                = v * sigmoid(2z)                    [0.5(1+tanh z) = sigmoid(2z)]
-//   with r = sigmoid(-2|z|) = e / (1 + e), e = exp(-2|z|) in (0, 1]:
-//     v >= 0 :  y = v (1 - r) = vh + (vl - vh r)      (small correction term)
-//     v <  0 :  y = v r                               (small result)
-//
+// Each takes x and the bias separately.  GELU_tanh is the hot one and is kept
+// cheap (see gelu_tanh_xb).  GELU_erf carries v = x + b exactly as (vh, vl) with
+// vh = fl(x + b) (Knuth's TwoSum), matching the reference's double sum, and is
+// evaluated through erfc so that the cancellation in (1 + erf) near -1 never
+// happens:
 //   GELU_erf(v) = 0.5 v (1 + erf(v / sqrt 2)) = 0.5 v erfc(-v / sqrt 2)
 //     v >= 0 :  y = vh + (vl - 0.5 vh erfc(v / sqrt 2))
 //     v <  0 :  y = 0.5 (vh + vl) erfc(-v / sqrt 2)
-//
-// so that the cancellation in (1 + tanh) or (1 + erf) near -1 never happens and
-// for large positive v the result is vh plus a tiny correction.
 // ---------------------------------------------------------------------------
 enum : int { kActNone = 0, kActRelu = 1, kActGeluErf = 2, kActGeluTanh = 3 };
 
@@ -78,19 +69,22 @@ __device__ __forceinline__ void two_sum(float a, float b, float& s, float& e) {
   e = (a - (s - bb)) + (b - bb);
 }
 
+// GELU_tanh(v) = 0.5 v (1 + tanh(z)), z = sqrt(2/pi) (v + 0.044715 v^3), evaluated
+// through 0.5 (1 + tanh z) = 1 / (1 + exp(-2z)) with the hardware base-2
+// exponential and reciprocal:  y = v * rcp(1 + 2^(v (c1 + c2 v^2))),
+// c1 = -2 log2(e) sqrt(2/pi), c2 = 0.044715 c1.  Seven VALU operations and two
+// transcendentals per element, so the kernel stays HBM-bound.  The limits come out
+// as the reference's formula gives them: v -> +inf gives +inf, v -> -inf gives
+// -inf * 0 = NaN, -0 gives -0, NaN propagates.  Against the double-precision
+// formula on float(x) + float(b) (v itself rounded once, as the reference kernel
+// rounds it) the error stays within a fifth of abs 1e-6 + rel 1e-6 over
+// |v| <= 30, also with the exponential and the reciprocal one ulp off.
 __device__ __forceinline__ float gelu_tanh_xb(float x, float b) {
-  float v, vl;
-  two_sum(x, b, v, vl);
-  const float u = v * v;
-  const float z = 0.7978845608028654f * __builtin_fmaf(0.044715f * v, u, v);
-  // e = exp(-2|z|) via the hardware base-2 exponential.
-  const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * __builtin_fabsf(z));
-  const float r = e * __builtin_amdgcn_rcpf(1.0f + e);
-  float y = (v >= 0.0f) ? v + __builtin_fmaf(-v, r, vl) : __builtin_fmaf(v, r, vl * r);
-  // Infinite v: TwoSum's error term is NaN there; the limits are +inf -> +inf and
-  // -inf -> 0 * inf = NaN, which is what the reference's formula gives.
-  if (__builtin_isinf(v)) y = (v > 0.0f) ? v : __builtin_nanf("");
-  return y;
+  constexpr float c1 = -2.30220818520f;    // -2 * log2(e) * sqrt(2/pi)
+  constexpr float c2 = -0.102943241596f;  // c1 * 0.044715
+  const float v = x + b;
+  const float a = v * __builtin_fmaf(c2, v * v, c1);
+  return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a));
 }
 
 __device__ __forceinline__ float gelu_erf_xb(float x, float b) {

@@ -217,18 +217,22 @@ using MfmaFn = void (*)(const float*, const float*, float*, int, int, int, float
                         int);
 
 // MFMA instantiations: (bm, bn, bk) with tm = bm/16, tn = bn/16 (256 lanes).
+// `even`: 16-byte path for M, N, K multiples of the tile (no bounds checks);
+// `vec`: 16-byte path with bounds checks; `scalar`: any shape and alignment.
 struct MfmaCfg {
   int bm, bn, bk;
-  MfmaFn vec, scalar;
+  MfmaFn even, vec, scalar;
 };
 
+#define MCKE_MFMA_CFG(BM, BN, BK)                                                     \
+  {BM, BN, BK, &gemm_mfma_kernel<BM, BN, BK, true, true>,                            \
+   &gemm_mfma_kernel<BM, BN, BK, true, false>, &gemm_mfma_kernel<BM, BN, BK, false, false>}
+
 const MfmaCfg kMfmaCfgs[] = {
-    {256, 256, 32, &gemm_mfma_kernel<256, 256, 32, true>, &gemm_mfma_kernel<256, 256, 32, false>},
-    {256, 256, 16, &gemm_mfma_kernel<256, 256, 16, true>, &gemm_mfma_kernel<256, 256, 16, false>},
-    {128, 128, 32, &gemm_mfma_kernel<128, 128, 32, true>, &gemm_mfma_kernel<128, 128, 32, false>},
-    {128, 128, 16, &gemm_mfma_kernel<128, 128, 16, true>, &gemm_mfma_kernel<128, 128, 16, false>},
-    {64, 64, 32, &gemm_mfma_kernel<64, 64, 32, true>, &gemm_mfma_kernel<64, 64, 32, false>},
+    MCKE_MFMA_CFG(256, 256, 32), MCKE_MFMA_CFG(256, 256, 16), MCKE_MFMA_CFG(128, 128, 32),
+    MCKE_MFMA_CFG(128, 128, 16), MCKE_MFMA_CFG(64, 64, 32),
 };
+#undef MCKE_MFMA_CFG
 
 const MfmaCfg* find_mfma(const mcke_gemm_tile& t) {
   for (const MfmaCfg& c : kMfmaCfgs)
@@ -240,9 +244,10 @@ struct Spec {
   const void* kernel = nullptr;   // for attribute queries
   GemmFn fn = nullptr;
   MfmaFn mfma = nullptr;
+  MfmaFn mfma_even = nullptr;     // unchecked 16-byte variant for whole tiles
   dim3 block{1, 1, 1};
   int threads = 0;
-  int tile_m = 0, tile_n = 0;
+  int tile_m = 0, tile_n = 0, tile_k = 0;
 };
 
 int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
@@ -298,6 +303,8 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
                        "(256,256,16,16,16), (128,128,32,8,8), (128,128,16,8,8) and "
                        "(64,64,32,4,4); no fallback is applied");
       s.mfma = vec4 ? cfg->vec : cfg->scalar;
+      s.mfma_even = vec4 ? cfg->even : nullptr;
+      s.tile_k = cfg->bk;
       s.block = dim3(kMfmaThreads, 1, 1);
       s.threads = kMfmaThreads;
       s.tile_m = cfg->bm;
@@ -309,7 +316,9 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
     default:
       return invalid("launch_gemm_f32: unknown GemmVariant " + std::to_string(variant));
   }
-  s.kernel = s.fn ? reinterpret_cast<const void*>(s.fn) : reinterpret_cast<const void*>(s.mfma);
+  // Attribute queries report the instantiation that whole-tile shapes run.
+  s.kernel = s.fn ? reinterpret_cast<const void*>(s.fn)
+                  : reinterpret_cast<const void*>(s.mfma_even ? s.mfma_even : s.mfma);
   return ok();
 }
 
@@ -384,7 +393,10 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
     const int64_t tiles_n = (n + sp.tile_n - 1) / sp.tile_n;
     if (tiles_m * tiles_n > 2147483647LL)
       return invalid("launch_gemm_f32: too many tiles for one launch");
-    sp.mfma<<<static_cast<unsigned>(tiles_m * tiles_n), sp.block, 0, s>>>(
+    const bool whole = sp.mfma_even && m % sp.tile_m == 0 && n % sp.tile_n == 0 &&
+                       k % sp.tile_k == 0;
+    const MfmaFn fn = whole ? sp.mfma_even : sp.mfma;
+    fn<<<static_cast<unsigned>(tiles_m * tiles_n), sp.block, 0, s>>>(
         a, b, c, mi, ni, ki, alpha, beta, static_cast<int>(tiles_m), static_cast<int>(tiles_n));
     MCKE_LAUNCH_CHECK("gemm_mfma_kernel");
     return ok();

@@ -170,7 +170,56 @@ struct MfmaStage {
   }
 };
 
-template <int BM, int BN, int BK, bool VEC>
+template <int BM, int BN, int BK>
+struct MfmaVecIO {
+  using S = MfmaStage<BM, BN, BK, true>;
+  static constexpr int kLoads = S::kAVec + S::kBVec;
+
+  // One of the stage's float4 loads: i < kAVec is A's i-th, else B's (i - kAVec)-th.
+  // EVEN (M, N, K multiples of the tile) drops the bounds checks.
+  template <bool EVEN>
+  static __device__ __forceinline__ void load_one(typename S::Regs& R, int i,
+                                                  const float* __restrict__ A,
+                                                  const float* __restrict__ B, int M, int N,
+                                                  int K, int m0, int n0, int k0) {
+    const int t = threadIdx.x;
+    if (i < S::kAVec) {
+      const int li = i * kMfmaThreads + t;
+      const int row = li / (BK / 4), c4 = li % (BK / 4);
+      const int gm = m0 + row, gk = k0 + 4 * c4;
+      if (EVEN || (gm < M && gk < K))
+        R.a[i] = *reinterpret_cast<const f32x4*>(A + static_cast<int64_t>(gm) * K + gk);
+      else
+        R.a[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      const int ib = i - S::kAVec;
+      const int li = ib * kMfmaThreads + t;
+      const int kr = li / (BN / 4), c4 = li % (BN / 4);
+      const int gk = k0 + kr, gn = n0 + 4 * c4;
+      if (EVEN || (gk < K && gn < N))
+        R.b[ib] = *reinterpret_cast<const f32x4*>(B + static_cast<int64_t>(gk) * N + gn);
+      else
+        R.b[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  static __device__ __forceinline__ void store_one(const typename S::Regs& R, int i,
+                                                   float* __restrict__ stage) {
+    const int t = threadIdx.x;
+    if (i < S::kAVec) {
+      const int li = i * kMfmaThreads + t;
+      const int row = li / (BK / 4), c4 = li % (BK / 4);
+      *reinterpret_cast<f32x4*>(stage + row * S::kLdA + 4 * c4) = R.a[i];
+    } else {
+      const int ib = i - S::kAVec;
+      const int li = ib * kMfmaThreads + t;
+      const int kr = li / (BN / 4), c4 = li % (BN / 4);
+      *reinterpret_cast<f32x4*>(stage + S::kAFloats + kr * S::kLdB + 4 * c4) = R.b[ib];
+    }
+  }
+};
+
+template <int BM, int BN, int BK, bool VEC, bool EVEN>
 __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
@@ -212,10 +261,24 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
   const int a_off = (wm * WM + c) * S::kLdA + h * (BK / 2);
   const int b_off = S::kAFloats + (h * (BK / 2)) * S::kLdB + wn * WN + NT * c;
 
+  // The next stage's global loads and LDS stores.  On the 16-byte path they are
+  // spread over the MFMA stream of the current stage -- loads over the first half
+  // of its P = BK/2 MFMA sub-steps, stores (into the other LDS buffer, free since
+  // the previous barrier) over the second half -- so the matrix pipe never waits
+  // for their issue.  The last stage re-loads itself (k0 clamped) and stores into
+  // the unused buffer: harmless, and it keeps the loop free of branches.
+  constexpr int P = BK / 2;
+  using IO = MfmaVecIO<BM, BN, BK>;
+  constexpr int L = IO::kLoads;
+
   for (int ks = 0; ks < ksteps; ++ks) {
     const float* stage = smem + (ks & 1) * S::kStageFloats;
+    float* next_stage = smem + ((ks + 1) & 1) * S::kStageFloats;
     const bool more = (ks + 1) < ksteps;
-    if (more) S::load(R, A, B, M, N, K, m0, n0, (ks + 1) * BK);
+    const int k_next = (more ? ks + 1 : ks) * BK;
+    if constexpr (!VEC) {
+      if (more) S::load(R, A, B, M, N, K, m0, n0, k_next);
+    }
 
     // LDS -> register fragments, software-pipelined one MFMA step ahead: the
     // reads for step (q, s+1) are issued before the MFMAs of step (q, s), so the
@@ -229,6 +292,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
     for (int q = 0; q < BK / 8; ++q) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
+        const int p = 4 * q + s;
         BV bv_next = bv;
         if (s < 3) {
           bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + s + 1) * S::kLdB);
@@ -238,6 +302,12 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
           for (int i = 0; i < MT; ++i)
             av_next[i] = *reinterpret_cast<const f32x4*>(stage + a_off + i * 32 * S::kLdA +
                                                          4 * (q + 1));
+        }
+        if constexpr (VEC) {
+#pragma unroll
+          for (int i = 0; i < L; ++i)
+            if ((i * (P / 2)) / L == p)
+              IO::template load_one<EVEN>(R, i, A, B, M, N, K, m0, n0, k_next);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -250,6 +320,11 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
           }
         }
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (VEC) {
+#pragma unroll
+          for (int i = 0; i < L; ++i)
+            if (P / 2 + (i * (P / 2)) / L == p) IO::store_one(R, i, next_stage);
+        }
         bv = bv_next;
         if (s == 3 && q + 1 < BK / 8) {
 #pragma unroll
@@ -258,7 +333,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
       }
     }
 
-    if (more) S::store(R, smem + ((ks + 1) & 1) * S::kStageFloats);
+    if constexpr (!VEC) {
+      if (more) S::store(R, next_stage);
+    }
     __syncthreads();
   }
 

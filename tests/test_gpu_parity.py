@@ -91,6 +91,21 @@ def test_bias_act_random(gpu, orc, act, shape):
             assert r.ok, f"vw={vw}: {r}"
 
 
+def test_bias_act_row_streaming_path_and_starved_grid(gpu, orc):
+    """More one-row workgroups than the small-launch limit: the row-per-workgroup
+    kernel, also with its row dimension capped (rows walked with a stride)."""
+    rows, cols = 4500, 1024
+    x = orc.fill_normal(rows * cols, 15)
+    b = orc.fill_random(cols, 16, -0.5, 0.5)
+    want = orc.bias_act(x, b, rows, cols, 3)
+    y4 = run_bias_act(gpu, x, b, rows, cols, 3, 4)
+    r = orc.compare(y4, want, 1e-6, 1e-6)
+    assert r.ok, str(r)
+    for vw, mrb in ((4, 7), (4, 4000), (1, 0), (2, 13)):
+        got = run_bias_act(gpu, x, b, rows, cols, 3, vw, max_row_blocks=mrb)
+        assert np.array_equal(golden_io.bits(got), golden_io.bits(y4)), (vw, mrb)
+
+
 def test_bias_act_width_invariance_and_starved_grid(gpu, orc):
     rows, cols = 300, 2048
     x = orc.fill_normal(rows * cols, 5)
@@ -147,9 +162,10 @@ def test_row_reduce_all_negative_and_inf_rows(gpu, orc):
 
 
 @pytest.mark.parametrize("variant", [0, 1])
-@pytest.mark.parametrize("cols", [1, 3, 17, 128, 131, 1024, 4096, 8192, 10000])
+@pytest.mark.parametrize("cols", [1, 3, 4, 17, 64, 128, 131, 200, 256, 512, 1024, 2048, 4096,
+                                  8192, 10000])
 def test_softmax_random(gpu, orc, variant, cols):
-    rows = 64 if cols <= 4096 else 8
+    rows = 67 if cols <= 4096 else 8          # ragged against every rows-per-workgroup
     x = orc.fill_normal(rows * cols, 0x50F7A11, 0.0, 2.0)
     x[5 * cols] += 30.0                                  # a spike row
     got = run_softmax(gpu, x, rows, cols, variant)
