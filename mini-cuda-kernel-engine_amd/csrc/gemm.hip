@@ -227,12 +227,17 @@ struct MfmaCfg {
 #define MCKE_MFMA_CFG(BM, BN, BK)                                                     \
   {BM, BN, BK, &gemm_mfma_kernel<BM, BN, BK, true, true>,                            \
    &gemm_mfma_kernel<BM, BN, BK, true, false>, &gemm_mfma_kernel<BM, BN, BK, false, false>}
+// BK = 32 whole tiles take the direct-to-LDS kernel.
+#define MCKE_MFMA_CFG_DMA(BM, BN)                                                     \
+  {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN>, &gemm_mfma_kernel<BM, BN, 32, true, false>, \
+   &gemm_mfma_kernel<BM, BN, 32, false, false>}
 
 const MfmaCfg kMfmaCfgs[] = {
-    MCKE_MFMA_CFG(256, 256, 32), MCKE_MFMA_CFG(256, 256, 16), MCKE_MFMA_CFG(128, 128, 32),
-    MCKE_MFMA_CFG(128, 128, 16), MCKE_MFMA_CFG(64, 64, 32),
+    MCKE_MFMA_CFG_DMA(256, 256), MCKE_MFMA_CFG(256, 256, 16), MCKE_MFMA_CFG_DMA(128, 128),
+    MCKE_MFMA_CFG(128, 128, 16), MCKE_MFMA_CFG_DMA(64, 64),
 };
 #undef MCKE_MFMA_CFG
+#undef MCKE_MFMA_CFG_DMA
 
 const MfmaCfg* find_mfma(const mcke_gemm_tile& t) {
   for (const MfmaCfg& c : kMfmaCfgs)
@@ -437,11 +442,15 @@ int mcke_gemm_kernel_attrs(int variant, const mcke_gemm_tile* tile, mcke_kernel_
 int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile* out) {
   if (!out) return invalid("gemm_mfma_default_tile: null out");
   (void)k;
-  // Largest tile that still gives every CU of a 256-CU part at least one tile.
-  const int64_t cus = 256;
+  // Largest tile that still gives every CU of a 256-CU part four tiles (one
+  // workgroup per CU at a time, so four rounds): measured on MI355X, 256 x 256
+  // wins at 8192^3 (1024 tiles), 128 x 128 at 4096^3 and 64 x 64 at 2048^3,
+  // each over the next larger tile with a single round.  Smaller problems take
+  // the smallest tile.
+  const int64_t want = 4 * 256;
   auto tiles = [&](int64_t t) { return ((m + t - 1) / t) * ((n + t - 1) / t); };
-  if (tiles(256) >= cus) *out = mcke_gemm_tile{256, 256, 32, 16, 16};
-  else if (tiles(128) >= cus) *out = mcke_gemm_tile{128, 128, 32, 8, 8};
+  if (tiles(256) >= want) *out = mcke_gemm_tile{256, 256, 32, 16, 16};
+  else if (tiles(128) >= want) *out = mcke_gemm_tile{128, 128, 32, 8, 8};
   else *out = mcke_gemm_tile{64, 64, 32, 4, 4};
   return ok();
 }

@@ -170,6 +170,48 @@ struct MfmaStage {
   }
 };
 
+// Epilogue shared by the MFMA kernels: C = alpha * acc + beta * C for the
+// workgroup's BM x BN tile (C is not read when beta == 0).  Lane (h, c) of wave
+// (wm, wn) holds, for MFMA tile (i, j) and accumulator register r, row
+// 8*(r/4) + 4h + r%4 of the tile's 32 rows and column NT*c + j of the wave's WN.
+template <int BM, int BN, bool VEC>
+__device__ __forceinline__ void mfma_store_c(const f32x16 (&acc)[BM / 64][BN / 64],
+                                             float* __restrict__ C, int M, int N, int m0, int n0,
+                                             int wm, int wn, int h, int c, float alpha,
+                                             float beta) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MT = WM / 32, NT = WN / 32;
+  const bool vec_store = VEC && (NT == 4) && ((N & 3) == 0);
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+      if (row >= M) continue;
+      const int col0 = n0 + wn * WN + NT * c;
+      float* crow = C + static_cast<int64_t>(row) * N;
+      float v[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) v[j] = alpha * acc[i][j][r];
+      if (vec_store && col0 + 3 < N) {
+        f32x4 o{v[0], v[NT > 1 ? 1 : 0], v[NT > 2 ? 2 : 0], v[NT > 3 ? 3 : 0]};
+        if (beta != 0.0f) o += beta * *reinterpret_cast<const f32x4*>(crow + col0);
+        *reinterpret_cast<f32x4*>(crow + col0) = o;
+      } else {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int col = col0 + j;
+          if (col < N) {
+            float o = v[j];
+            if (beta != 0.0f) o += beta * crow[col];
+            crow[col] = o;
+          }
+        }
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int BK>
 struct MfmaVecIO {
   using S = MfmaStage<BM, BN, BK, true>;
@@ -339,36 +381,173 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
     __syncthreads();
   }
 
-  // Epilogue: C = alpha * acc + beta * C (C is not read when beta == 0).
-  const bool vec_store = VEC && (NT == 4) && ((N & 3) == 0);
+  mfma_store_c<BM, BN, VEC>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
+}
+
+
+// ---------------------------------------------------------------------------
+// Whole-tile variant with direct-to-LDS loads (gfx950 global_load_lds_dwordx4).
+//
+// For M % BM == N % BN == K % 32 == 0 and 16-byte aligned A and B.  The next
+// stage is fetched straight from global memory into the other LDS buffer: no
+// VGPR staging, no ds_write, and no wait on the loads until the step's closing
+// barrier.  One such instruction writes its 64 lanes' 16 bytes to 1 KB of
+// contiguous LDS (lane j at byte 16 j of a wave-uniform base), so the layouts are
+// chosen per 1 KB chunk:
+//   B (BK x BN, row-major, unpadded): chunk c holds elements [256 c, 256 c + 256)
+//     of the stage, lane j the float4 at element 256 c + 4 j;
+//   A (BM x 32, 128-byte rows, unpadded): chunk c holds rows 8c .. 8c+7; the
+//     float4 at position p of row r holds k-slot p ^ f(r), f(r) = (r & 7) ^
+//     ((r >> 3) & 1).  The MFMA fragment reads fetch one k-slot from 32
+//     consecutive rows; the swizzle puts any 8 (or 16) consecutive rows of a slot
+//     on distinct 16-byte bank groups, so they are conflict-free without padding.
+// ---------------------------------------------------------------------------
+// Issues direct-to-LDS instruction i of a wave's share of one stage (A chunks
+// first, then B chunks) for K columns [k0, k0 + 32): 16 bytes per lane into the
+// wave-uniform 1 KB chunk of `stage` that the instruction owns.
+template <int NA, int NB, int kAFloats>
+__device__ __forceinline__ void mfma_dma_issue(int i, const float* const (&srcA)[NA],
+                                               const float* const (&srcB)[NB], int64_t stepB,
+                                               float* stage, int k0, int wave) {
+  if (i < NA) {
+    __builtin_amdgcn_global_load_lds(srcA[i] + k0, stage + (wave * NA + i) * 256, 16, 0, 0);
+  } else {
+    const int ib = i - NA;
+    __builtin_amdgcn_global_load_lds(srcB[ib] + static_cast<int64_t>(k0 / 32) * stepB,
+                                     stage + kAFloats + (wave * NB + ib) * 256, 16, 0, 0);
+  }
+}
+
+template <int BM, int BN>
+__global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
+    int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
+  constexpr int BK = 32;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MT = WM / 32, NT = WN / 32;
+  static_assert(MT >= 1 && (NT == 1 || NT == 2 || NT == 4), "unsupported wave tile");
+  constexpr int kAFloats = BM * BK;
+  constexpr int kStageFloats = kAFloats + BK * BN;
+  constexpr int kAChunks = kAFloats / 256, kBChunks = BK * BN / 256;   // 1 KB chunks
+  constexpr int NA = kAChunks / 4, NB = kBChunks / 4;                   // per wave
+  static_assert(kAChunks % 4 == 0 && kBChunks % 4 == 0, "chunks must split over 4 waves");
+  constexpr int L = NA + NB;            // DMA instructions per wave per stage
+  constexpr int P = BK / 2;             // MFMA sub-steps per stage
+  using BV = typename BVec<NT>::type;
+
+  __shared__ __attribute__((aligned(16))) float smem[2 * kStageFloats];
+
+  int tm, tn;
+  mfma_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int wm = wave / 2, wn = wave % 2;
+  const int h = lane / 32, c = lane % 32;
+
+  // This lane's source addresses for its wave's chunks of stage 0 (advanced by BK
+  // columns of A and BK rows of B per stage).
+  const int jr = lane / 8, jp = lane % 8;
+  const float* srcA[NA];
+  const float* srcB[NB];
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
+  for (int ii = 0; ii < NA; ++ii) {
+    const int ch = wave * NA + ii;
+    const int row = 8 * ch + jr;
+    const int slot = jp ^ jr ^ (ch & 1);          // f(row) = jr ^ (ch & 1)
+    srcA[ii] = A + static_cast<int64_t>(m0 + row) * K + 4 * slot;
+  }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-      if (row >= M) continue;
-      const int col0 = n0 + wn * WN + NT * c;
-      float* crow = C + static_cast<int64_t>(row) * N;
-      float v[NT];
+  for (int ii = 0; ii < NB; ++ii) {
+    const int e = (wave * NB + ii) * 256 + 4 * lane;
+    srcB[ii] = B + static_cast<int64_t>(e / BN) * N + n0 + e % BN;
+  }
+  const int64_t stepB = static_cast<int64_t>(BK) * N;
+
+  f32x16 acc[MT][NT];
 #pragma unroll
-      for (int j = 0; j < NT; ++j) v[j] = alpha * acc[i][j][r];
-      if (vec_store && col0 + 3 < N) {
-        f32x4 o{v[0], v[NT > 1 ? 1 : 0], v[NT > 2 ? 2 : 0], v[NT > 3 ? 3 : 0]};
-        if (beta != 0.0f) o += beta * *reinterpret_cast<const f32x4*>(crow + col0);
-        *reinterpret_cast<f32x4*>(crow + col0) = o;
-      } else {
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          const int col = col0 + j;
-          if (col < N) {
-            float o = v[j];
-            if (beta != 0.0f) o += beta * crow[col];
-            crow[col] = o;
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int ksteps = K / BK;
+  if (ksteps > 0) {
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+      mfma_dma_issue<NA, NB, kAFloats>(i, srcA, srcB, stepB, smem, 0, wave);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // Fragment addressing: rows wm*WM + i*32 + c all share f = f(c) (the row base
+  // is a multiple of 16); k-slot 4h + q sits at position (4h + q) ^ f.
+  const int f = (c & 7) ^ ((c >> 3) & 1);
+  const int a_row = (wm * WM + c) * BK;
+  int a_q[BK / 8];
+#pragma unroll
+  for (int q = 0; q < BK / 8; ++q) a_q[q] = 4 * ((4 * h + q) ^ f);
+  const int b_off = kAFloats + (h * (BK / 2)) * BN + wn * WN + NT * c;
+
+  for (int ks = 0; ks < ksteps; ++ks) {
+    const float* stage = smem + (ks & 1) * kStageFloats;
+    float* next_stage = smem + ((ks + 1) & 1) * kStageFloats;
+    // The last stage re-fetches itself into the idle buffer (kept branch-free).
+    const int k_next = ((ks + 1) < ksteps ? ks + 1 : ks) * BK;
+
+    f32x4 av[MT], av_next[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      av[i] = *reinterpret_cast<const f32x4*>(stage + a_row + i * 32 * BK + a_q[0]);
+    BV bv = *reinterpret_cast<const BV*>(stage + b_off);
+#pragma unroll
+    for (int q = 0; q < BK / 8; ++q) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int p = 4 * q + s;
+        BV bv_next = bv;
+        if (s < 3) {
+          bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + s + 1) * BN);
+        } else if (q + 1 < BK / 8) {
+          bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + 4) * BN);
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+            av_next[i] =
+                *reinterpret_cast<const f32x4*>(stage + a_row + i * 32 * BK + a_q[q + 1]);
+        }
+        // The next stage's DMA instructions, spread over the first half of the
+        // sub-steps so that their issue hides under the MFMAs.
+#pragma unroll
+        for (int i = 0; i < L; ++i)
+          if ((i * (P / 2)) / L == p)
+            mfma_dma_issue<NA, NB, kAFloats>(i, srcA, srcB, stepB, next_stage, k_next, wave);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j) {
+            float bj;
+            if constexpr (NT == 1) bj = bv; else bj = bv[j];
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], bj, acc[i][j], 0, 0, 0);
           }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        bv = bv_next;
+        if (s == 3 && q + 1 < BK / 8) {
+#pragma unroll
+          for (int i = 0; i < MT; ++i) av[i] = av_next[i];
         }
       }
     }
+    // The DMA writes land in LDS when vmcnt drops; the barrier then publishes them
+    // and retires every wave's reads of `stage` before it is refilled.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
   }
+
+  mfma_store_c<BM, BN, true>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
 }
 
 }  // namespace mcke_amd
