@@ -33,20 +33,39 @@ template <class T> __device__ __forceinline__ void st_stream(T* p, T v) {
 }
 
 // ---------------------------------------------------------------------------
-// Wave64 butterfly reductions.  Every lane ends with the same bits: at each step
-// lane i forms op(v_i, v_{i^m}) and lane i^m forms op(v_{i^m}, v_i), and both
-// ops are commutative.
+// Wave64 group reductions over WIDTH consecutive lanes (WIDTH a power of two).
+// The steps inside 16-lane rows use DPP lane permutations (a few cycles each)
+// instead of ds_bpermute (an LDS-pipe round trip each):
+//   pairs        quad_perm [1,0,3,2]
+//   quads        quad_perm [2,3,0,1]
+//   8 lanes      row_half_mirror (lane i <-> 7 - i: pairs the two quads)
+//   16 lanes     row_mirror      (lane i <-> 15 - i: pairs the two halves)
+// and the steps across rows use __shfl_xor 16 / 32.  Every lane ends with the
+// same bits: each step combines a lane with a partner holding the same partial
+// set, op(a, b) on one side and op(b, a) on the other, and both ops commute.
 // ---------------------------------------------------------------------------
-template <int WIDTH = 64> __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                            0xF, 0xF, true));
+}
+
+template <int WIDTH, class Op> __device__ __forceinline__ float wave_reduce(float v, Op op) {
+  static_assert(WIDTH >= 1 && WIDTH <= 64 && (WIDTH & (WIDTH - 1)) == 0, "power of two");
+  if constexpr (WIDTH >= 2) v = op(v, dpp_mov<0xB1>(v));    // quad_perm [1,0,3,2]
+  if constexpr (WIDTH >= 4) v = op(v, dpp_mov<0x4E>(v));    // quad_perm [2,3,0,1]
+  if constexpr (WIDTH >= 8) v = op(v, dpp_mov<0x141>(v));   // row_half_mirror
+  if constexpr (WIDTH >= 16) v = op(v, dpp_mov<0x140>(v));  // row_mirror
+  if constexpr (WIDTH >= 32) v = op(v, __shfl_xor(v, 16, 64));
+  if constexpr (WIDTH >= 64) v = op(v, __shfl_xor(v, 32, 64));
   return v;
 }
 
+template <int WIDTH = 64> __device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce<WIDTH>(v, [](float a, float b) { return a + b; });
+}
+
 template <int WIDTH = 64> __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = WIDTH / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  return wave_reduce<WIDTH>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // ---------------------------------------------------------------------------

@@ -32,11 +32,15 @@ namespace mcke_amd {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLoadUnroll = 4;
-// kTwoPass sizing: aim for ~4 workgroups per CU on a 256-CU part (measured best
-// for the full-tensor sum: fewer partials for pass 2, no tail), but never give a
-// workgroup fewer than kMinColsPerBlock columns of one row.
-constexpr int64_t kTargetBlocks = 1024;
+constexpr int kLoadUnroll = 4;      // loads in flight per lane, one-pass kernels
+constexpr int kPass1Unroll = 8;     // loads in flight per lane, kTwoPass pass 1
+// kTwoPass sizing: one workgroup per CU on a 256-CU part, each lane keeping 8
+// float4 loads in flight.  Measured on the full-tensor sum of 2^26 floats
+// (pass 1 + pass 2): 42.1 us at 256 x 8, 42.3 us at 512 x 4, 43.6 us at
+// 1024 x 4, 45.5 us at 2048 x 4 -- more workgroups buy nothing in pass 1 and
+// cost pass 2.  A workgroup never gets fewer than kMinColsPerBlock columns of
+// one row.
+constexpr int64_t kTargetBlocks = 256;
 constexpr int64_t kMinColsPerBlock = 4096;
 constexpr int64_t kMaxSplit = 65535;
 
@@ -58,34 +62,34 @@ template <class Op> __device__ __forceinline__ float fold4(f32x4 v) {
 
 // Partial of x[begin, end) for this thread, lanes striding by kThreads.
 // VEC: begin and end are multiples of 4 and x is 16-byte aligned.
-template <class Op, bool VEC>
+template <class Op, bool VEC, int U = kLoadUnroll>
 __device__ __forceinline__ float thread_partial(const float* __restrict__ x, int64_t begin,
                                                 int64_t end) {
   float acc = Op::identity();
   if constexpr (VEC) {
     const f32x4* __restrict__ xv = reinterpret_cast<const f32x4*>(x);
     const int64_t b4 = begin >> 2, e4 = end >> 2;
-    for (int64_t i = b4 + threadIdx.x; i < e4; i += kLoadUnroll * kThreads) {
-      f32x4 a[kLoadUnroll];
+    for (int64_t i = b4 + threadIdx.x; i < e4; i += U * kThreads) {
+      f32x4 a[U];
 #pragma unroll
-      for (int u = 0; u < kLoadUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         const int64_t j = i + u * kThreads;
         if (j < e4) a[u] = ld_stream(xv + j);
       }
 #pragma unroll
-      for (int u = 0; u < kLoadUnroll; ++u)
+      for (int u = 0; u < U; ++u)
         if (i + u * kThreads < e4) acc = Op::apply(acc, fold4<Op>(a[u]));
     }
   } else {
-    for (int64_t i = begin + threadIdx.x; i < end; i += kLoadUnroll * kThreads) {
-      float a[kLoadUnroll];
+    for (int64_t i = begin + threadIdx.x; i < end; i += U * kThreads) {
+      float a[U];
 #pragma unroll
-      for (int u = 0; u < kLoadUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         const int64_t j = i + u * kThreads;
         if (j < end) a[u] = ld_stream(x + j);
       }
 #pragma unroll
-      for (int u = 0; u < kLoadUnroll; ++u)
+      for (int u = 0; u < U; ++u)
         if (i + u * kThreads < end) acc = Op::apply(acc, a[u]);
     }
   }
@@ -142,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void row_reduce_pass1_kernel(
   int64_t end = begin + chunk;
   if (end > cols) end = cols;
   float v = Op::identity();
-  if (begin < end) v = thread_partial<Op, VEC>(x + r * cols, begin, end);
+  if (begin < end) v = thread_partial<Op, VEC, kPass1Unroll>(x + r * cols, begin, end);
   v = block_combine_shfl<Op>(v);
   if (threadIdx.x == 0) ws[r * split + s] = v;
 }

@@ -174,7 +174,7 @@ TEST(launchers_reject_bad_arguments_without_launching) {
   const Status st = K::launch_gemm_f32(X, B, Y, 8, 8, 8, 1.f, 0.f, K::GemmVariant::kTiledSmem, K::GemmTile{}, s);
   CHECK(st.code() == StatusCode::kInvalidArgument && st.message().find("no fallback") != std::string::npos);
   CHECK(K::max_vector_width_f32(X, 4096) == 4 && K::max_vector_width_f32(X, 4094) == 2);
-  CHECK(K::row_reduce_workspace_bytes(1, 1 << 26, K::ReduceVariant::kTwoPass) == 1024 * 4);
+  CHECK(K::row_reduce_workspace_bytes(1, 1 << 26, K::ReduceVariant::kTwoPass) == 256 * 4);
   CHECK(K::mfma_default_tile(8192, 8192, 8192).bm == 256);
 }
 

@@ -108,8 +108,8 @@ def test_workspace_query(mcke):
     assert mcke.row_reduce_workspace_bytes(8192, 8192, mcke.ReduceVariant.kWarpShuffle) == 0
     assert mcke.row_reduce_workspace_bytes(0, 100, TP) == 0
     assert mcke.row_reduce_workspace_bytes(8192, 8192, TP) == 8192 * 4          # split 1
-    assert mcke.row_reduce_workspace_bytes(1, 1 << 26, TP) == 1024 * 4          # full sum
-    assert mcke.row_reduce_workspace_bytes(64, 524288, TP) == 64 * 16 * 4
+    assert mcke.row_reduce_workspace_bytes(1, 1 << 26, TP) == 256 * 4           # full sum
+    assert mcke.row_reduce_workspace_bytes(64, 524288, TP) == 64 * 4 * 4
     assert mcke.row_reduce_workspace_bytes(1, 1000, TP) == 4                    # short row
 
 
