@@ -32,8 +32,10 @@ enum mcke_memory_policy {
   MCKE_MEM_REUSE_SAME_STREAM = 2,
   MCKE_MEM_REUSE_HAPPENS_BEFORE = 3
 };
-/* Allocator behind the executor's arena and workspaces. */
-enum mcke_allocator_kind { MCKE_ALLOC_RAW = 0, MCKE_ALLOC_BUDDY = 1 };
+/* Allocator behind the executor's arena and workspaces: RawDeviceAllocator,
+ * BuddyAllocator (buddy_allocator.hpp) or FreeListAllocator (freelist_allocator.hpp),
+ * each with its default configuration. */
+enum mcke_allocator_kind { MCKE_ALLOC_RAW = 0, MCKE_ALLOC_BUDDY = 1, MCKE_ALLOC_FREELIST = 2 };
 
 /* ExecutorOptions (executor.hpp:115-134). */
 typedef struct mcke_executor_options {

@@ -37,6 +37,7 @@ class MemoryPolicy(enum.IntEnum):        # memory_plan.hpp
 class AllocatorKind(enum.IntEnum):
     kRaw = 0
     kBuddy = 1
+    kFreeList = 2
 
 
 class ExecutorOptions(C.Structure):

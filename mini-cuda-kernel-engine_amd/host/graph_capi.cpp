@@ -6,6 +6,7 @@
 
 #include "mcke/graph/executor.hpp"
 #include "mcke/memory/buddy_allocator.hpp"
+#include "mcke/memory/freelist_allocator.hpp"
 #include "mcke_graph.h"
 
 struct mcke_graph {
@@ -142,6 +143,8 @@ int mcke_executor_create(mcke_graph* g, int allocator_kind, const mcke_executor_
   auto e = std::make_unique<mcke_executor>();
   if (allocator_kind == MCKE_ALLOC_BUDDY)
     e->alloc = std::make_unique<mcke::BuddyAllocator>();
+  else if (allocator_kind == MCKE_ALLOC_FREELIST)
+    e->alloc = std::make_unique<mcke::FreeListAllocator>();
   else if (allocator_kind == MCKE_ALLOC_RAW)
     e->alloc = std::make_unique<mcke::RawDeviceAllocator>();
   else

@@ -24,6 +24,7 @@
 #include "mcke/kernels/kernels.hpp"
 #include "mcke/kernels/softmax_online.hpp"
 #include "mcke/memory/buddy_allocator.hpp"
+#include "mcke/memory/freelist_allocator.hpp"
 #include "mcke/profiling/profiler.hpp"
 
 using namespace mcke;
@@ -614,6 +615,190 @@ TEST(buddy_growth_bypass_and_trim) {
   CHECK_OK(b.validate());
   CHECK_OK(b.deallocate(*a, s1));
   CHECK(b.deallocate(*a, s1).code() == StatusCode::kInvalidArgument);   // double free
+}
+
+// ---------------------------------------------------------------------------
+// FreeList allocator on host memory with fake streams.
+class HostFreeList : public FreeListAllocator {
+ public:
+  using FreeListAllocator::FreeListAllocator;
+  mutable std::set<rt::StreamHandle> busy;
+  int raw_allocs = 0, raw_frees = 0;
+
+ protected:
+  bool stream_completed(rt::StreamHandle s) const override { return busy.count(s) == 0; }
+  void wait_stream(rt::StreamHandle s) const override { busy.erase(s); }
+  StatusOr<void*> raw_alloc(std::size_t bytes) override {
+    ++raw_allocs;
+    void* p = std::aligned_alloc(256, bytes);
+    if (!p) return OutOfMemoryError("host aligned_alloc failed");
+    return p;
+  }
+  void raw_free(void* p) override {
+    ++raw_frees;
+    std::free(p);
+  }
+};
+
+static FreeListConfig fl_cfg(ReusePolicy p) {
+  FreeListConfig c;
+  c.slab_bytes = 4 << 20;
+  c.small_class_granularity = 512;
+  c.small_large_split = 64 << 10;
+  c.large_alloc_threshold = 2 << 20;
+  c.reuse_policy = p;
+  return c;
+}
+
+TEST(freelist_size_classes) {
+  HostFreeList f(fl_cfg(ReusePolicy::kCoarseStreamPoll));
+  CHECK_OK(f.config_status());
+  // 128 linear classes of 512 B up to 64 KiB, then 128, 256, ..., 2048 KiB.
+  CHECK_EQ(f.size_class_of(1), std::size_t{0});
+  CHECK_EQ(f.size_class_of(512), std::size_t{0});
+  CHECK_EQ(f.size_class_of(513), std::size_t{1});
+  CHECK_EQ(f.size_class_of(64 << 10), std::size_t{127});
+  CHECK_EQ(f.size_class_of((64 << 10) + 1), std::size_t{128});
+  CHECK_EQ(f.size_class_of(128 << 10), std::size_t{128});
+  CHECK_EQ(f.size_class_of((128 << 10) + 1), std::size_t{129});
+  CHECK_EQ(f.size_class_of(2 << 20), std::size_t{132});
+  CHECK_EQ(f.num_classes(), std::size_t{133});
+  for (std::size_t c = 0; c < f.num_classes(); ++c) {
+    const std::size_t b = f.class_block_bytes(c);
+    CHECK_EQ(f.size_class_of(b), c);                          // a block is the top of its class
+    if (c > 0) CHECK(f.size_class_of(f.class_block_bytes(c - 1) + 1) == c);
+  }
+  FreeListConfig bad = fl_cfg(ReusePolicy::kCoarseStreamPoll);
+  bad.small_class_granularity = 384;
+  HostFreeList g(bad);
+  CHECK(g.config_status().code() == StatusCode::kInvalidArgument);
+  CHECK(g.allocate(100, fake_stream(1)).status().code() == StatusCode::kInvalidArgument);
+}
+
+TEST(freelist_carve_cache_reuse) {
+  HostFreeList f(fl_cfg(ReusePolicy::kCoarseStreamPoll));
+  const auto s1 = fake_stream(1);
+  auto a = f.allocate(1000, s1);
+  CHECK(a.ok() && a->bytes == 1024 && a->requested_bytes == 1000);
+  CHECK(reinterpret_cast<std::uintptr_t>(a->ptr) % 256 == 0);
+  auto b = f.allocate(100 << 10, s1);                         // class 128 KiB
+  CHECK(b.ok() && b->bytes == std::size_t{128 << 10});
+  CHECK_EQ(f.raw_allocs, 1);
+  CHECK_EQ(f.stats().bytes_in_use, std::size_t{1024 + (128 << 10)});
+  CHECK_OK(f.validate());
+  CHECK_OK(f.deallocate(*a, s1));
+  auto c = f.allocate(600, s1);                               // same class, same stream
+  CHECK(c.ok() && c->ptr == a->ptr);
+  CHECK_EQ(f.stats().reuse_hits, std::uint64_t{1});
+  auto d = f.allocate(1000, s1);                              // cache empty: carved anew
+  CHECK(d.ok() && d->ptr != a->ptr);
+  CHECK_OK(f.validate());
+  CHECK_OK(f.deallocate(*b, s1));
+  CHECK_OK(f.deallocate(*c, s1));
+  CHECK_OK(f.deallocate(*d, s1));
+  CHECK(f.deallocate(*d, s1).code() == StatusCode::kFailedPrecondition);   // double free
+  CHECK_OK(f.validate());
+  CHECK_EQ(f.stats().bytes_in_use, std::size_t{0});
+}
+
+TEST(freelist_stream_ordered_reuse) {
+  for (ReusePolicy pol : {ReusePolicy::kSameStreamOnly, ReusePolicy::kCoarseStreamPoll}) {
+    HostFreeList f(fl_cfg(pol));
+    const auto s1 = fake_stream(1), s2 = fake_stream(2);
+    auto a = f.allocate(64 << 10, s1);
+    void* first = a->ptr;
+    f.busy.insert(s1);
+    CHECK_OK(f.deallocate(*a, s1));
+    CHECK_EQ(f.stats().deferred_reuses, std::uint64_t{1});
+    auto on_s1 = f.allocate(64 << 10, s1);                    // same stream: safe at once
+    CHECK(on_s1->ptr == first);
+    CHECK_OK(f.deallocate(*on_s1, s1));
+    auto on_s2 = f.allocate(64 << 10, s2);                    // s1 busy: never the same bytes
+    CHECK(on_s2->ptr != first);
+    CHECK_OK(f.deallocate(*on_s2, s2));
+    f.busy.erase(s1);
+    auto later = f.allocate(64 << 10, s2);
+    if (pol == ReusePolicy::kCoarseStreamPoll)
+      CHECK(later->ptr == first || later->ptr == on_s2->ptr);   // both blocks are reusable now
+    else
+      CHECK(later->ptr == on_s2->ptr);                         // only s2's own block
+    CHECK_OK(f.validate());
+  }
+}
+
+TEST(freelist_split_blocking_drain_and_oom) {
+  FreeListConfig cfg = fl_cfg(ReusePolicy::kCoarseStreamPoll);
+  cfg.split_large_blocks = true;
+  cfg.max_total_bytes = 4 << 20;
+  HostFreeList f(cfg);
+  const auto s1 = fake_stream(1), s2 = fake_stream(2);
+  auto big = f.allocate(2 << 20, s1);                         // 2 MiB class
+  CHECK(big.ok());
+  CHECK_OK(f.deallocate(*big, s1));
+  // A 1 MiB request on the same stream cuts its block from the cached 2 MiB one;
+  // the 1 MiB tail is cached in its own class.
+  auto half = f.allocate(1 << 20, s1);
+  CHECK(half.ok() && half->ptr == big->ptr && half->bytes == std::size_t{1 << 20});
+  auto tail = f.allocate(1 << 20, s1);
+  CHECK(tail.ok() && static_cast<char*>(tail->ptr) == static_cast<char*>(big->ptr) + (1 << 20));
+  CHECK_EQ(f.raw_allocs, 1);
+  CHECK_OK(f.validate());
+  // Fill the rest of the only slab the cap allows, park a block behind busy s1,
+  // and ask on s2: the allocator waits for s1 (a counted blocking drain).
+  auto rest = f.allocate(2 << 20, s1);
+  CHECK(rest.ok());
+  f.busy.insert(s1);
+  CHECK_OK(f.deallocate(*rest, s1));
+  auto again = f.allocate(2 << 20, s2);
+  CHECK(again.ok() && again->ptr == rest->ptr);
+  CHECK_EQ(f.stats().blocking_drains, std::uint64_t{1});
+  auto none = f.allocate(512, s2);                            // slab full, cap reached
+  CHECK(!none.ok() && none.status().code() == StatusCode::kOutOfMemory);
+  CHECK_EQ(f.stats().oom_events, std::uint64_t{1});
+  CHECK_OK(f.deallocate(*half, s1));
+  CHECK_OK(f.deallocate(*tail, s1));
+  CHECK_OK(f.deallocate(*again, s2));
+  CHECK_OK(f.validate());
+}
+
+TEST(freelist_bypass_trim_and_random_walk) {
+  HostFreeList f(fl_cfg(ReusePolicy::kCoarseStreamPoll));
+  const auto s1 = fake_stream(1), s2 = fake_stream(2);
+  auto big = f.allocate(8 << 20, s1);                         // above the 2 MiB threshold
+  CHECK(big.ok() && big->slab_id == kBypassSlabId && big->bytes == std::size_t{8 << 20});
+  CHECK_OK(f.deallocate(*big, s1));
+  CHECK_EQ(f.raw_frees, 1);
+  // Random walk over sizes and streams; validate() after every step.
+  std::uint64_t rng = 0x1234567;
+  auto next = [&] { rng = rng * 6364136223846793005ULL + 1442695040888963407ULL; return rng >> 33; };
+  std::vector<std::pair<Allocation, rt::StreamHandle>> held;
+  for (int step = 0; step < 400; ++step) {
+    if (held.size() < 24 && (next() % 3 != 0 || held.empty())) {
+      const std::size_t sz = 1 + next() % (next() % 4 == 0 ? (2 << 20) : (48 << 10));
+      const auto st = (next() & 1) ? s1 : s2;
+      auto a = f.allocate(sz, st);
+      CHECK(a.ok());
+      if (a.ok()) {
+        CHECK(a->bytes >= sz && a->bytes == f.class_block_bytes(f.size_class_of(sz)));
+        held.emplace_back(*a, st);
+      }
+    } else {
+      const std::size_t i = next() % held.size();
+      CHECK_OK(f.deallocate(held[i].first, held[i].second));
+      held.erase(held.begin() + static_cast<std::ptrdiff_t>(i));
+    }
+    CHECK_OK(f.validate());
+  }
+  for (auto& [a, st] : held) CHECK_OK(f.deallocate(a, st));
+  CHECK_EQ(f.stats().bytes_in_use, std::size_t{0});
+  const int frees_before = f.raw_frees;
+  CHECK_OK(f.trim());                                         // every slab is empty: all released
+  CHECK(f.raw_frees > frees_before);
+  CHECK_EQ(f.stats().bytes_reserved, std::size_t{0});
+  CHECK_OK(f.validate());
+  auto fresh = f.allocate(4096, s1);                          // a new slab after the trim
+  CHECK(fresh.ok());
+  CHECK_OK(f.deallocate(*fresh, s1));
 }
 
 TEST(first_bit_mismatch_helper) {

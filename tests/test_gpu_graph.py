@@ -139,9 +139,30 @@ def test_level_parallel_event_counts(G):
     assert info["num_events"] == 12 and info["waits_dedup"] == 36
 
 
-def test_buddy_allocator_reuses_across_plans(G, orc):
+def test_allocators_give_same_bits(G, orc):
+    """The arena's allocator changes addresses, never results."""
+    T, D, F = 128, 64, 256
+    inp = _mlp_inputs(orc, T, D, F)
+    outs = []
+    for kind in (G.AllocatorKind.kRaw, G.AllocatorKind.kBuddy, G.AllocatorKind.kFreeList):
+        g, t = G.mlp_block(T, D, F)
+        ex = G.Executor(g, allocator=kind, schedule=G.SchedulePolicy.kChainGreedy,
+                        memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=3,
+                        poison_buffers=True)
+        ex.plan()
+        for k, v in inp.items():
+            ex.set_input(t[k], v)
+        ex.run_sync()
+        outs.append(ex.read(t["y"], T * D))
+        ex.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["kBuddy", "kFreeList"])
+def test_allocator_reuses_across_plans(G, orc, kind):
     g, t = G.mlp_block(128, 64, 256)
-    ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, num_streams=2)
+    ex = G.Executor(g, allocator=getattr(G.AllocatorKind, kind), num_streams=2)
     ex.plan()
     first = ex.allocator_stats()
     ex.plan()                      # re-plan: the old arena returns, the new one reuses it
