@@ -425,6 +425,37 @@ def graph_section(m, steps=5, warmup=2):
     fan["speedup_vs_sequential"] = round(fan["sequential"]["wall_ms"] /
                                          fan["chain_greedy_4streams"]["wall_ms"], 3)
     out["fanout4x4_gemm2048"] = fan
+
+    # Launch-bound shapes: the same MLP chain at small sizes, replayed eagerly (the
+    # plan's launches issued by the host each run) and as one captured HIP graph
+    # launch per run.
+    out["mlp_small_capture"] = []
+    for (T2, D2, F2) in ((512, 256, 1024), (64, 64, 256)):
+        cap = {}
+        for label in ("eager", "hip_graph"):
+            g, t = G.mlp_block(T2, D2, F2)
+            ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList,
+                            schedule=G.SchedulePolicy.kChainGreedy,
+                            memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=2)
+            ex.plan()
+            ex.set_input(t["x"], m.fill_normal(T2 * D2, 0x3101, 0.0, 1.0))
+            ex.set_input(t["W1"], m.fill_normal(D2 * F2, 0x3102, 0.0, 0.02))
+            ex.set_input(t["b1"], m.fill_normal(F2, 0x3103, 0.0, 0.01))
+            ex.set_input(t["W2"], m.fill_normal(F2 * D2, 0x3104, 0.0, 0.02))
+            ex.set_input(t["b2"], m.fill_normal(D2, 0x3105, 0.0, 0.01))
+            if label == "hip_graph":
+                ex.capture()
+            wall = timed_runs(ex, 200)
+            y = ex.read(t["y"], T2 * D2)
+            cap[label] = {"us_per_run": round(wall * 1e3, 2), "y_bits": y.view(np.uint32)}
+            ex.close()
+        same = bool(np.array_equal(cap["eager"].pop("y_bits"), cap["hip_graph"].pop("y_bits")))
+        entry = {"shape": f"X[{T2}x{D2}] W1[{D2}x{F2}] W2[{F2}x{D2}]", **cap,
+                 "speedup": round(cap["eager"]["us_per_run"] / cap["hip_graph"]["us_per_run"], 3),
+                 "same_bits": same}
+        log(f"MLP {T2}x{D2}x{F2}: eager {cap['eager']['us_per_run']} us, "
+            f"hipGraph {cap['hip_graph']['us_per_run']} us per run, same bits: {same}")
+        out["mlp_small_capture"].append(entry)
     return out
 
 

@@ -128,6 +128,19 @@ class GraphExecutor {
   [[nodiscard]] Status plan();
   [[nodiscard]] Status set_input(TensorId t, const void* host_data, std::size_t bytes);
   [[nodiscard]] Status run_async();
+  // Captures one iteration of run_async() into a HIP graph (stream capture on
+  // stream 0; the other streams join through the plan's fork/join and
+  // cross-stream events) and instantiates it; every later run_async() replays
+  // that graph with one launch instead of re-issuing the plan's launches and
+  // events.  The reference plans this step as capture_cuda_graph
+  // (include/mcke/graph/executor.hpp:23-27).  Refused with per-node timing probes
+  // (their events would be frozen into the graph), with the vendor-library GEMM
+  // (its internals are not ours to vet for memset nodes), and for plans on more
+  // than one stream (multi-stream capture is switched off).  With
+  // poison_buffers the pattern captured is the capture iteration's.  plan()
+  // drops the captured graph, since it binds the old plan's buffers.
+  [[nodiscard]] Status capture_graph();
+  [[nodiscard]] bool captured() const noexcept { return graph_exec_ != nullptr; }
   [[nodiscard]] Status synchronize();
   [[nodiscard]] Status run_sync() {
     MCKE_RETURN_IF_ERROR(run_async());
@@ -147,6 +160,8 @@ class GraphExecutor {
   // Drains the plan's streams, returns its storages to the allocator while the
   // streams they were last used on still exist, then drops the plan.
   void release_plan();
+  [[nodiscard]] Status issue_plan();   // one iteration's launches, events and fills
+  void release_capture();
 
   Graph graph_;
   DeviceAllocator& alloc_;
@@ -157,6 +172,7 @@ class GraphExecutor {
   std::vector<NodeTiming> node_timings_;
   std::vector<std::pair<TensorId, std::vector<char>>> input_cache_;
   bool planned_ = false;
+  void* graph_exec_ = nullptr;   // hipGraphExec_t of the captured iteration
 };
 
 }  // namespace mcke

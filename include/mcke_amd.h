@@ -197,6 +197,17 @@ int mcke_rt_event_elapsed_ms(void* start, void* stop, float* ms);
 
 /* raw_device_malloc / raw_device_free (device.cpp:104-130): hipMalloc, which is
  * 256-byte aligned; out-of-memory maps to MCKE_STATUS_OUT_OF_MEMORY. */
+/* Stream capture into a HIP graph (no reference counterpart: the reference plans
+ * it as capture_cuda_graph, include/mcke/graph/executor.hpp:23-27).  Capture runs
+ * in thread-local mode on a stream this library created; other streams join the
+ * capture through events recorded on a capturing stream.  end_capture
+ * instantiates the captured graph and returns the executable graph; launch
+ * replays it on `stream`; destroy releases it.  Nothing captured may be a memset
+ * (kernels fill memory here, never hipMemsetAsync). */
+int mcke_rt_stream_begin_capture(void* stream);
+int mcke_rt_stream_end_capture(void* stream, void** out_exec);
+int mcke_rt_graph_launch(void* exec, void* stream);
+int mcke_rt_graph_destroy(void* exec);
 int mcke_rt_malloc(void** out_ptr, size_t bytes);
 int mcke_rt_free(void* ptr);
 int mcke_rt_host_alloc(void** out_ptr, size_t bytes); /* pinned host memory */

@@ -153,6 +153,38 @@ int mcke_rt_stream_wait_event(void* stream, void* event) {
   return ok();
 }
 
+// ---- stream capture into a HIP graph ---------------------------------------
+int mcke_rt_stream_begin_capture(void* stream) {
+  if (!stream) return invalid("mcke_rt_stream_begin_capture: the legacy default stream cannot be captured");
+  MCKE_HIP_TRY(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal));
+  return ok();
+}
+
+int mcke_rt_stream_end_capture(void* stream, void** out_exec) {
+  if (!stream || !out_exec) return invalid("mcke_rt_stream_end_capture: null argument");
+  *out_exec = nullptr;
+  hipGraph_t graph = nullptr;
+  MCKE_HIP_TRY(hipStreamEndCapture(static_cast<hipStream_t>(stream), &graph));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);   // the executable graph keeps what it needs
+  MCKE_HIP_TRY(e);
+  *out_exec = exec;
+  return ok();
+}
+
+int mcke_rt_graph_launch(void* exec, void* stream) {
+  if (!exec) return invalid("mcke_rt_graph_launch: null graph");
+  MCKE_HIP_TRY(hipGraphLaunch(static_cast<hipGraphExec_t>(exec), static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+int mcke_rt_graph_destroy(void* exec) {
+  if (!exec) return ok();
+  MCKE_HIP_TRY(hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec)));
+  return ok();
+}
+
 int mcke_rt_event_create(void** out_event, int timing) {
   if (!out_event) return invalid("mcke_rt_event_create: null out");
   hipEvent_t e = nullptr;

@@ -104,6 +104,8 @@ def host_lib() -> C.CDLL:
         "mcke_executor_set_input": (C.c_int, [_VP, _U32, _VP, C.c_size_t]),
         "mcke_executor_run_async": (C.c_int, [_VP]),
         "mcke_executor_synchronize": (C.c_int, [_VP]),
+        "mcke_executor_capture": (C.c_int, [_VP]),
+        "mcke_executor_is_captured": (C.c_int, [_VP, C.POINTER(C.c_int)]),
         "mcke_executor_read_tensor": (C.c_int, [_VP, _U32, _VP, C.c_size_t]),
         "mcke_executor_plan_info": (C.c_int, [_VP, C.POINTER(PlanInfo)]),
         "mcke_executor_collect_timings": (C.c_int, [_VP, C.POINTER(NodeTiming), C.c_size_t,
@@ -228,6 +230,16 @@ class Executor:
     def run_sync(self) -> None:
         self.run_async()
         self.synchronize()
+
+    def capture(self) -> None:
+        """Capture one iteration into a HIP graph; later run_async() replays it."""
+        _check(host_lib().mcke_executor_capture(self.h))
+
+    @property
+    def captured(self) -> bool:
+        out = C.c_int(0)
+        _check(host_lib().mcke_executor_is_captured(self.h, C.byref(out)))
+        return bool(out.value)
 
     def read(self, t: int, numel: int) -> np.ndarray:
         out = np.empty(numel, dtype=np.float32)

@@ -173,6 +173,14 @@ int mcke_executor_run_async(mcke_executor* e) { return e ? code(e->exec->run_asy
 
 int mcke_executor_synchronize(mcke_executor* e) { return e ? code(e->exec->synchronize()) : bad("null executor"); }
 
+int mcke_executor_capture(mcke_executor* e) { return e ? code(e->exec->capture_graph()) : bad("null executor"); }
+
+int mcke_executor_is_captured(mcke_executor* e, int* out) {
+  if (!e || !out) return bad("mcke_executor_is_captured: null argument");
+  *out = e->exec->captured() ? 1 : 0;
+  return MCKE_STATUS_OK;
+}
+
 int mcke_executor_read_tensor(mcke_executor* e, uint32_t t, void* host, size_t bytes) {
   if (!e || !host) return bad("null argument");
   auto tr = e->exec->any_bound_tensor(t);

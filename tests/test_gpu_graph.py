@@ -173,3 +173,109 @@ def test_allocator_reuses_across_plans(G, orc, kind):
     info = ex.plan_info()
     assert info["arena_bytes"] <= info["naive_bytes"]
     assert s["bytes_in_use"] >= info["arena_bytes"]
+
+
+# ---------------------------------------------------------------------------
+# HIP graph capture of the replay loop
+# ---------------------------------------------------------------------------
+def _eager_y(G, inp, T, D, F, **kw):
+    g, t = G.mlp_block(T, D, F)
+    ex = G.Executor(g, **kw)
+    ex.plan()
+    for k, v in inp.items():
+        ex.set_input(t[k], v)
+    ex.run_sync()
+    y = ex.read(t["y"], T * D)
+    ex.close()
+    return y
+
+
+@pytest.mark.parametrize("poison", [False, True])
+def test_captured_replays_match_eager(G, orc, poison):
+    """Every replay of the captured iteration gives the eager bits, with the
+    program's own eager work and synchronisations between replays; new inputs
+    written with set_input are seen by the replays."""
+    import mcke_amd as m
+    T, D, F = 256, 128, 512
+    kw = dict(schedule=G.SchedulePolicy.kChainGreedy, memory=G.MemoryPolicy.kReuseHappensBefore,
+              num_streams=4, poison_buffers=poison)
+    inp = _mlp_inputs(orc, T, D, F)
+    gold = _eager_y(G, inp, T, D, F, **kw)
+    g, t = G.mlp_block(T, D, F)
+    ex = G.Executor(g, **kw)
+    ex.plan()
+    for k, v in inp.items():
+        ex.set_input(t[k], v)
+    ex.capture()
+    assert ex.captured
+    scratch_x = m.DeviceBuffer.from_array(orc.fill_normal(4096, 9))
+    scratch_y = m.DeviceBuffer(4096 * 4)
+    for rep in range(4):
+        ex.run_sync()
+        got = ex.read(t["y"], T * D)
+        assert np.array_equal(got.view(np.uint32), gold.view(np.uint32)), f"replay {rep}"
+        # unrelated eager work between replays
+        m.launch_activation_f32(scratch_x, scratch_y, 4096, m.Activation.kGeluTanh, 4).throw_if_error()
+        m.device_synchronize()
+    inp2 = dict(inp, x=orc.fill_normal(T * D, 77, 0.0, 1.0))
+    gold2 = _eager_y(G, inp2, T, D, F, **kw)
+    ex.set_input(t["x"], inp2["x"])
+    for rep in range(2):
+        ex.run_sync()
+        assert np.array_equal(ex.read(t["y"], T * D).view(np.uint32), gold2.view(np.uint32))
+    ex.plan()                              # a new plan binds new buffers: capture dropped
+    assert not ex.captured
+    ex.close()
+
+
+@pytest.mark.skip(reason="multi-stream capture is switched off: its one run ended in a host "
+                         "segfault inside the HIP runtime, cause not shown in this code")
+def test_captured_fanout_across_streams(G, orc):
+    n, B, Dp = 128, 4, 3
+    g, t = G.gemm_fanout(B, Dp, n)
+    ex = G.Executor(g, schedule=G.SchedulePolicy.kLevelParallel,
+                    memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4)
+    ex.plan()
+    w = (orc.fill_random(n * n, 7) * 0.0625).astype(np.float32)
+    xs = [orc.fill_random(n * n, 300 + k) for k in range(B)]
+    ex.set_input(t["W"], w)
+    for k in range(B):
+        ex.set_input(t["xs"][k], xs[k])
+    ex.run_sync()
+    eager = [ex.read(t["outs"][k], n * n) for k in range(B)]
+    ex.capture()
+    for rep in range(3):
+        ex.run_sync()
+        for k in range(B):
+            got = ex.read(t["outs"][k], n * n)
+            assert np.array_equal(got.view(np.uint32), eager[k].view(np.uint32)), (rep, k)
+    for k in range(B):
+        want = xs[k]
+        for _ in range(Dp):
+            want = orc.gemm(want, w, np.zeros(n * n, np.float32), n, n, n)
+        r = orc.compare(eager[k], want, 1e-4, 1e-5)
+        assert r.ok, f"branch {k}: {r}"
+    ex.close()
+
+
+def test_capture_refused_for_multi_stream_plans(G):
+    """The refusal is checked on the host before any capture call is made."""
+    g, _ = G.gemm_fanout(4, 2, 64)
+    ex = G.Executor(g, schedule=G.SchedulePolicy.kChainGreedy, num_streams=4)
+    ex.plan()
+    assert ex.plan_info()["num_streams_used"] == 4
+    with pytest.raises(Exception, match="single-stream"):
+        ex.capture()
+    assert not ex.captured
+    ex.run_sync()                          # the eager path is unaffected
+    ex.close()
+
+
+def test_capture_refused_with_timing_probes(G):
+    g, _ = G.mlp_block(64, 64, 64)
+    ex = G.Executor(g, num_streams=2, profile=True)
+    ex.plan()
+    with pytest.raises(Exception, match="FailedPrecondition|timing probes"):
+        ex.capture()
+    assert not ex.captured
+    ex.close()
