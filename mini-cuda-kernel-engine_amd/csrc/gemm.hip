@@ -228,13 +228,13 @@ struct MfmaCfg {
   {BM, BN, BK, &gemm_mfma_kernel<BM, BN, BK, true, true>,                            \
    &gemm_mfma_kernel<BM, BN, BK, true, false>, &gemm_mfma_kernel<BM, BN, BK, false, false>}
 // BK = 32 whole tiles take the direct-to-LDS kernel.
-#define MCKE_MFMA_CFG_DMA(BM, BN)                                                     \
-  {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN>, &gemm_mfma_kernel<BM, BN, 32, true, false>, \
+#define MCKE_MFMA_CFG_DMA(BM, BN, ST)                                                 \
+  {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST>, &gemm_mfma_kernel<BM, BN, 32, true, false>, \
    &gemm_mfma_kernel<BM, BN, 32, false, false>}
 
 const MfmaCfg kMfmaCfgs[] = {
-    MCKE_MFMA_CFG_DMA(256, 256), MCKE_MFMA_CFG(256, 256, 16), MCKE_MFMA_CFG_DMA(128, 128),
-    MCKE_MFMA_CFG(128, 128, 16), MCKE_MFMA_CFG_DMA(64, 64),
+    MCKE_MFMA_CFG_DMA(256, 256, 2), MCKE_MFMA_CFG(256, 256, 16), MCKE_MFMA_CFG_DMA(128, 128, 2),
+    MCKE_MFMA_CFG(128, 128, 16), MCKE_MFMA_CFG_DMA(64, 64, 2),
 };
 #undef MCKE_MFMA_CFG
 #undef MCKE_MFMA_CFG_DMA

@@ -405,20 +405,19 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
 // Issues direct-to-LDS instruction i of a wave's share of one stage (A chunks
 // first, then B chunks) for K columns [k0, k0 + 32): 16 bytes per lane into the
 // wave-uniform 1 KB chunk of `stage` that the instruction owns.
-template <int NA, int NB, int kAFloats>
-__device__ __forceinline__ void mfma_dma_issue(int i, const float* const (&srcA)[NA],
-                                               const float* const (&srcB)[NB], int64_t stepB,
-                                               float* stage, int k0, int wave) {
-  if (i < NA) {
-    __builtin_amdgcn_global_load_lds(srcA[i] + k0, stage + (wave * NA + i) * 256, 16, 0, 0);
+__device__ __forceinline__ void mfma_dma_issue(int i, int na, int nb, int a_floats,
+                                               const float* const* srcA, const float* const* srcB,
+                                               int64_t stepB, float* stage, int k0, int wave) {
+  if (i < na) {
+    __builtin_amdgcn_global_load_lds(srcA[i] + k0, stage + (wave * na + i) * 256, 16, 0, 0);
   } else {
-    const int ib = i - NA;
+    const int ib = i - na;
     __builtin_amdgcn_global_load_lds(srcB[ib] + static_cast<int64_t>(k0 / 32) * stepB,
-                                     stage + kAFloats + (wave * NB + ib) * 256, 16, 0, 0);
+                                     stage + a_floats + (wave * nb + ib) * 256, 16, 0, 0);
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int STAGES>
 __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
@@ -434,8 +433,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
   constexpr int L = NA + NB;            // DMA instructions per wave per stage
   constexpr int P = BK / 2;             // MFMA sub-steps per stage
   using BV = typename BVec<NT>::type;
+  static_assert(STAGES >= 2 && (STAGES - 2) * L <= 63, "vmcnt counts at most 63 loads");
 
-  __shared__ __attribute__((aligned(16))) float smem[2 * kStageFloats];
+  __shared__ __attribute__((aligned(16))) float smem[STAGES * kStageFloats];
 
   int tm, tn;
   mfma_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
@@ -474,13 +474,18 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   const int ksteps = K / BK;
+  // Prologue: stages 0 .. STAGES-2 in flight.  Past the last K step a stage
+  // re-fetches the last one into a buffer nobody reads, which keeps the number of
+  // loads per stage -- and so the vmcnt arithmetic below -- uniform.
   if (ksteps > 0) {
 #pragma unroll
-    for (int i = 0; i < L; ++i)
-      mfma_dma_issue<NA, NB, kAFloats>(i, srcA, srcB, stepB, smem, 0, wave);
+    for (int st = 0; st < STAGES - 1; ++st) {
+      const int kk = (st < ksteps ? st : ksteps - 1) * BK;
+#pragma unroll
+      for (int i = 0; i < L; ++i)
+        mfma_dma_issue(i, NA, NB, kAFloats, srcA, srcB, stepB, smem + st * kStageFloats, kk, wave);
+    }
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
 
   // Fragment addressing: rows wm*WM + i*32 + c all share f = f(c) (the row base
   // is a multiple of 16); k-slot 4h + q sits at position (4h + q) ^ f.
@@ -492,10 +497,22 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
   const int b_off = kAFloats + (h * (BK / 2)) * BN + wn * WN + NT * c;
 
   for (int ks = 0; ks < ksteps; ++ks) {
-    const float* stage = smem + (ks & 1) * kStageFloats;
-    float* next_stage = smem + ((ks + 1) & 1) * kStageFloats;
-    // The last stage re-fetches itself into the idle buffer (kept branch-free).
-    const int k_next = ((ks + 1) < ksteps ? ks + 1 : ks) * BK;
+    // Stage ks has landed once at most the (STAGES - 2) younger stages' loads are
+    // still outstanding; the barrier then publishes every wave's share of it and
+    // retires every wave's reads of the buffer that the next fetch overwrites
+    // (the one read in step ks - 1).
+    // A bare s_barrier: __syncthreads() would also drain every outstanding load
+    // (vmcnt(0)), which serialises the pipeline.  Each wave's ds_reads of the
+    // buffer being refilled were already waited on by the MFMAs that used them,
+    // and the asm statements keep the compiler from moving memory accesses
+    // across the barrier.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - 2) * L) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const float* stage = smem + (ks % STAGES) * kStageFloats;
+    float* next_stage = smem + ((ks + STAGES - 1) % STAGES) * kStageFloats;
+    const int kf = ks + STAGES - 1;
+    const int k_next = (kf < ksteps ? kf : ksteps - 1) * BK;
 
     f32x4 av[MT], av_next[MT];
 #pragma unroll
@@ -517,12 +534,12 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
             av_next[i] =
                 *reinterpret_cast<const f32x4*>(stage + a_row + i * 32 * BK + a_q[q + 1]);
         }
-        // The next stage's DMA instructions, spread over the first half of the
-        // sub-steps so that their issue hides under the MFMAs.
+        // The fetch of stage ks + STAGES - 1, spread over the first half of the
+        // sub-steps so that its issue hides under the MFMAs.
 #pragma unroll
         for (int i = 0; i < L; ++i)
           if ((i * (P / 2)) / L == p)
-            mfma_dma_issue<NA, NB, kAFloats>(i, srcA, srcB, stepB, next_stage, k_next, wave);
+            mfma_dma_issue(i, NA, NB, kAFloats, srcA, srcB, stepB, next_stage, k_next, wave);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
@@ -541,11 +558,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
         }
       }
     }
-    // The DMA writes land in LDS when vmcnt drops; the barrier then publishes them
-    // and retires every wave's reads of `stage` before it is refilled.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
   }
+  // No LDS DMA may still be landing when the workgroup retires.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   mfma_store_c<BM, BN, true>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
 }
