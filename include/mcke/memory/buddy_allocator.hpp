@@ -57,6 +57,8 @@ class BuddyAllocator : public DeviceAllocator {
   [[nodiscard]] Status validate() const override;
   [[nodiscard]] std::string dump_free_map() const;
   [[nodiscard]] const BuddyConfig& config() const noexcept { return cfg_; }
+  // Freed blocks still waiting for their stream or event before reuse.
+  [[nodiscard]] std::size_t parked_count() const noexcept { return parked_.size(); }
 
  protected:
   // Completion seams (tests substitute fake streams through these).

@@ -72,6 +72,8 @@ class FreeListAllocator : public DeviceAllocator {
   [[nodiscard]] std::size_t num_classes() const { return cache_.size(); }
   [[nodiscard]] std::string dump_free_map() const;
   [[nodiscard]] const FreeListConfig& config() const noexcept { return cfg_; }
+  // Freed blocks still waiting for their stream or event before reuse.
+  [[nodiscard]] std::size_t parked_count() const noexcept { return parked_.size(); }
   // Status of the configuration (every call fails with it when it is invalid).
   [[nodiscard]] Status config_status() const { return config_status_; }
 
