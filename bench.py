@@ -25,9 +25,13 @@ Also measured in the same run: the denominators (fp32 MFMA peak sustained for
 about the GEMM's duration, a STREAM triad), the GEMM size sweep, the config-5
 graph section and the CPU baseline.
 
+The CPU leg (skipped with --no-cpu) checks every op's output at its timed shape
+against the CPU oracle (ops[*].parity: the GEMM by the reference's 1024-entry spot
+check, the others element by element at BASELINE's tolerances), then times the
+CPU reference of the same GEMM on a bounded row slab (`cpu_baseline`).
+
 Printed: one JSON line (rank 0, N = 1).  `value` is the GEMM's TFLOP/s; `ops` lists
-every kernel with its roofline fraction; `roofline` is the GEMM's; `cpu_baseline`
-times the CPU reference of the same GEMM on a bounded row slab.
+every kernel with its roofline fraction; `roofline` is the GEMM's.
 """
 from __future__ import annotations
 
@@ -83,6 +87,8 @@ class Op:
         self.total_ms = 0.0
         self.launches = 0
         self.single_ms: list[float] = []
+        self.verify = None       # callable(oracle) -> dict, run in the CPU leg
+        self.parity = None
 
     def summary(self, measured_peak=None, traffic=None):
         avg = self.total_ms / self.launches
@@ -107,6 +113,8 @@ class Op:
             out["frac_of_measured"] = round(achieved / measured_peak, 4)
         if traffic is not None:
             out["hbm_traffic_bytes"] = traffic
+        if self.parity is not None:
+            out["parity"] = self.parity
         return out
 
 
@@ -153,31 +161,65 @@ def build_ops(m, stream, only=None):
             a, b, c, n, n, n, 1.0, 0.0, m.GemmVariant.kMfmaF32, tile, st)),
             "mfma", 2 * n * n * n, "flop", f"{n}x{n}x{n} tile {tile.astuple()}"))
 
+        def verify_gemm(orc):
+            ha, hb, hc = a.download(n * n), b.download(n * n), c.download(n * n)
+            r = orc.spot_check_gemm(ha, hb, hc, n, n, n, 1.0, 1024, 0x5A11E, orc.tol_gemm(n),
+                                    orc.abs_tol_gemm(n))
+            return {"ok": r.checked == 1024 and r.mismatches == 0, "max_abs_err": r.max_abs_err,
+                    "max_rel_err": r.max_rel_err,
+                    "check": "1024-entry spot check in double (reference.hpp:401-426), rel "
+                             f"tol_gemm({n}) + abs abs_tol_gemm({n})"}
+        ops[-1].verify = verify_gemm
+
     # --- reductions --------------------------------------------
     R = C_ = 8192
     if want("row_sum") or want("row_max"):
         log("generating reduce input (8192^2 N(0,1))")
         red_bytes = (R * C_ + R) * 4
         sets = rotation_sets(red_bytes)
-        xr = copies(m.fill_normal(R * C_, 0x5EED12345), sets)
-        outr = outputs(R * 4, sets)
+        hx = m.fill_normal(R * C_, 0x5EED12345)
+        xr = copies(hx, sets)
         for kind, nm in ((m.ReduceKind.kSum, "row_sum"), (m.ReduceKind.kMax, "row_max")):
             if want(nm):
-                ops.append(Op(nm, (lambda i, kind=kind, s=sets: ck(m.launch_row_reduce_f32(
+                outr = outputs(R * 4, sets)
+                ops.append(Op(nm, (lambda i, kind=kind, s=sets, outr=outr: ck(m.launch_row_reduce_f32(
                     xr[i % s], outr[i % s], R, C_, kind, m.ReduceVariant.kWarpShuffle, st))),
                     "hbm", red_bytes, "byte", f"{R}x{C_}", sets))
+
+                def verify_reduce(orc, kind=kind, outr=outr):
+                    got = outr[0].download(R)
+                    want_ = orc.row_reduce(hx, R, C_, int(kind))
+                    if int(kind) == 1:
+                        ok = bool(np.array_equal(got, want_))
+                        return {"ok": ok, "check": "bit-exact against the double-accumulating CPU max"}
+                    # the reference's term-magnitude floor (reference.hpp:312-321) for N(0,1) rows
+                    floor = 5e-5 * (1.0 / 0.577) * np.sqrt(C_ / 4096.0)
+                    r = orc.compare(got, want_, 1e-5, floor)
+                    return {"ok": bool(r.ok), "max_abs_err": r.max_abs_err,
+                            "max_rel_err": r.max_rel_err,
+                            "check": f"every row, rel 1e-5 + abs {floor:.3g}"}
+                ops[-1].verify = verify_reduce
     N26 = 1 << 26
     if want("full_sum"):
         log("generating full-sum input (2^26 U[0,1))")
         fs_bytes = (N26 + 1) * 4
         sets = rotation_sets(fs_bytes)
-        xs = copies(m.fill_random(N26, 0xF011, 0.0, 1.0), sets)
+        hxs = m.fill_random(N26, 0xF011, 0.0, 1.0)
+        xs = copies(hxs, sets)
         wsb = m.row_reduce_workspace_bytes(1, N26, m.ReduceVariant.kTwoPass)
         ws, outs = D(wsb), D(4)
         keep += [ws, outs]
         ops.append(Op("full_sum", lambda i, s=sets: ck(m.launch_row_reduce_f32(
             xs[i % s], outs, 1, N26, m.ReduceKind.kSum, m.ReduceVariant.kTwoPass, ws, wsb, st)),
             "hbm", fs_bytes, "byte", "1x2^26", sets))
+
+        def verify_full(orc):
+            got = float(outs.download(1)[0])
+            want_ = float(orc.row_reduce(hxs, 1, N26, 0)[0])
+            rel = abs(got - want_) / abs(want_)
+            return {"ok": rel <= 1e-5, "max_rel_err": rel, "got": got, "want": want_,
+                    "check": "rel 1e-5 against the double-accumulating CPU sum"}
+        ops[-1].verify = verify_full
 
     # --- softmax -----------------------------------------------
     rows = 32768
@@ -197,6 +239,16 @@ def build_ops(m, stream, only=None):
                                      m.SoftmaxVariant.kOnlineOnePass, st))),
             "hbm", sm_bytes, "byte", f"{rows}x{cols}", sets))
 
+        def verify_softmax(orc, x=x, dy=dy, cols=cols):
+            got = dy[0].download(rows * cols)
+            r = orc.compare(got, orc.row_softmax(x, rows, cols), 1e-5, 1e-6)
+            sums = got.reshape(rows, cols).astype(np.float64).sum(axis=1)
+            dev = float(np.max(np.abs(sums - 1.0)))
+            return {"ok": bool(r.ok) and dev <= 1e-5, "max_abs_err": r.max_abs_err,
+                    "max_row_sum_dev": dev,
+                    "check": "every element abs 1e-6 / rel 1e-5; every row sum within 1e-5"}
+        ops[-1].verify = verify_softmax
+
     # --- bias + GELU(tanh) -------------------------------------
     for (br, bc) in ((16384, 4096), (4096, 1024)):
         if not want(f"bias_gelu_{br}x{bc}"):
@@ -204,13 +256,20 @@ def build_ops(m, stream, only=None):
         log(f"generating bias+GELU input ({br}x{bc})")
         bg_bytes = (2 * br * bc + bc) * 4
         sets = rotation_sets(bg_bytes)
-        dx = copies(m.fill_normal(br * bc, 0xB1A5AC7 + br), sets)
-        db = copies(m.fill_random(bc, 0xB1A5B1A5, -0.5, 0.5), sets)
+        hxb = m.fill_normal(br * bc, 0xB1A5AC7 + br)
+        hbb = m.fill_random(bc, 0xB1A5B1A5, -0.5, 0.5)
+        dx, db = copies(hxb, sets), copies(hbb, sets)
         dy = outputs(br * bc * 4, sets)
         ops.append(Op(f"bias_gelu_{br}x{bc}", (lambda i, dx=dx, db=db, dy=dy, br=br, bc=bc, s=sets: ck(
             m.launch_bias_act_f32(dx[i % s], db[i % s], dy[i % s], br, bc,
                                   m.Activation.kGeluTanh, 4, st))),
             "hbm", bg_bytes, "byte", f"{br}x{bc}", sets))
+
+        def verify_bias(orc, hxb=hxb, hbb=hbb, dy=dy, br=br, bc=bc):
+            r = orc.compare(dy[0].download(br * bc), orc.bias_act(hxb, hbb, br, bc, 3), 1e-6, 1e-6)
+            return {"ok": bool(r.ok), "max_abs_err": r.max_abs_err, "max_rel_err": r.max_rel_err,
+                    "check": "every element abs 1e-6 + rel 1e-6 against the double GELU_tanh"}
+        ops[-1].verify = verify_bias
 
     # --- calibration: a plain copy of known size (only when asked for) -------
     if only is not None and want("copy_256mib"):
@@ -511,7 +570,7 @@ def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-sweep", action="store_true", help="skip the GEMM size sweep")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -542,7 +601,7 @@ def main(argv=None) -> int:
     log(f"timed: {args.steps} steps")
     total_ms = run_steps(m, stream, ops, args.steps, record=True)
     log("timed region done; single-launch diagnostic pass")
-    single_launches(m, stream, ops, min(args.steps, 10))
+    single_launches(m, stream, ops, min(args.steps, 20))
 
     peaks = None
     if not args.no_peaks and only is None:
@@ -561,12 +620,24 @@ def main(argv=None) -> int:
 
     sweep = [] if (args.no_sweep or only is not None) else gemm_sweep(m, stream)
     graph_res = None if (args.no_graph or only is not None) else graph_section(m)
-    gemm = summaries[0]
     cpu = None
+    if not args.no_cpu:
+        # The CPU checker on every timed op's output at its timed shape (the timed
+        # launches wrote these buffers); results land in ops[*].parity.
+        import oracle
+        for op in ops:
+            if op.verify is not None:
+                t0 = time.perf_counter()
+                op.parity = op.verify(oracle)
+                log(f"parity {op.name}: {'OK' if op.parity['ok'] else 'FAILED'} "
+                    f"({time.perf_counter() - t0:.1f} s)")
     if not args.no_cpu and gemm_bufs[0] is not None:
         log(f"cpu baseline: reference GEMM on a row slab (~{args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(m, gemm_bufs, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} TFLOP/s ({cpu['sample']})")
+    summaries = [op.summary(s["measured_peak"] if "measured_peak" in s else None,
+                            s.get("hbm_traffic_bytes")) for op, s in zip(ops, summaries)]
+    gemm = summaries[0]
 
     line = {
         "metric": METRIC,
