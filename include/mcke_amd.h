@@ -170,6 +170,33 @@ int mcke_gemm_kernel_attrs(int variant, const mcke_gemm_tile* tile,
  * (the callers that do not hand-pick a tile: the graph layer, the benchmark). */
 int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile* out);
 
+/* ---- 16-bit-input GEMM on the matrix cores -------------------------------
+ * No counterpart in the reference: its DType enum reserves kF16 and kBF16 for
+ * matrix-unit inputs (include/mcke/core/dtype.hpp:33-41, values below) but the
+ * only GEMM launcher is fp32 (kernels.hpp:265-269).  Callers: those with 16-bit
+ * weights and activations (the graph layer's next dtype, the benchmark). */
+enum mcke_dtype { MCKE_DTYPE_F32 = 0, MCKE_DTYPE_F16 = 1, MCKE_DTYPE_BF16 = 2 };
+
+/* C = alpha * A B + beta * C; A (m x k) and B (k x n) row-major in ab_dtype
+ * (MCKE_DTYPE_BF16 or MCKE_DTYPE_F16), products accumulated in fp32
+ * (v_mfma_f32_32x32x16_{bf16,f16}), C row-major in c_dtype (MCKE_DTYPE_F32 or
+ * ab_dtype, rounded to nearest even).  Validation as mcke_launch_gemm_f32: m or
+ * n == 0 is a no-op, k == 0 gives C = beta * C, C is not read when beta == 0,
+ * a == c / b == c and negative or > INT32_MAX extents are INVALID_ARGUMENT.
+ * Tiles (bm,bn,bk,tm,tn): (256,256,64,16,16), (128,128,64,8,8), (64,64,64,4,4);
+ * any other tile is INVALID_ARGUMENT.  Any shape and alignment is accepted;
+ * k % 8 == 0, n % 8 == 0 and 16-byte aligned a, b, c take the 16-byte path. */
+int mcke_launch_gemm_lp(const void* a, const void* b, void* c, int ab_dtype, int c_dtype,
+                        int64_t m, int64_t n, int64_t k, float alpha, float beta,
+                        const mcke_gemm_tile* tile, void* stream);
+
+/* mcke_gemm_kernel_attrs for the whole-tile kernel of one (dtype pair, tile). */
+int mcke_gemm_lp_kernel_attrs(int ab_dtype, int c_dtype, const mcke_gemm_tile* tile,
+                              mcke_kernel_attrs* out);
+
+/* The tile this build picks for a 16-bit GEMM of this shape. */
+int mcke_gemm_lp_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile* out);
+
 /* ---- runtime: rt::Stream / rt::Event / raw device memory ------------------
  * reference include/mcke/runtime/stream.hpp:82-306, src/core/device.cpp:56-168,
  * src/memory/allocator.cpp:44-73, src/tensor/tensor.cpp:108-138. */

@@ -78,6 +78,12 @@ class GemmVariant(enum.IntEnum):         # gemm_tile.hpp:209-214, append-only
     kMfmaF32 = 8                         # appended: fp32 MFMA (gfx950)
 
 
+class DType(enum.IntEnum):               # include/mcke/core/dtype.hpp:33-41 (first three)
+    kF32 = 0
+    kF16 = 1
+    kBF16 = 2
+
+
 class GemmTile(C.Structure):             # gemm_tile.hpp:47-69
     _fields_ = [("bm", C.c_int32), ("bn", C.c_int32), ("bk", C.c_int32),
                 ("tm", C.c_int32), ("tn", C.c_int32)]
@@ -179,6 +185,11 @@ def lib() -> C.CDLL:
         "mcke_gemm_kernel_attrs": (C.c_int, [C.c_int, C.POINTER(GemmTile),
                                              C.POINTER(KernelAttrs)]),
         "mcke_gemm_mfma_default_tile": (C.c_int, [_I64, _I64, _I64, C.POINTER(GemmTile)]),
+        "mcke_launch_gemm_lp": (C.c_int, [_VP, _VP, _VP, C.c_int, C.c_int, _I64, _I64, _I64,
+                                          C.c_float, C.c_float, C.POINTER(GemmTile), _VP]),
+        "mcke_gemm_lp_kernel_attrs": (C.c_int, [C.c_int, C.c_int, C.POINTER(GemmTile),
+                                                C.POINTER(KernelAttrs)]),
+        "mcke_gemm_lp_default_tile": (C.c_int, [_I64, _I64, _I64, C.POINTER(GemmTile)]),
         "mcke_rt_get_device_count": (C.c_int, [C.POINTER(C.c_int)]),
         "mcke_rt_set_device": (C.c_int, [C.c_int]),
         "mcke_rt_get_device": (C.c_int, [C.POINTER(C.c_int)]),
@@ -496,6 +507,30 @@ def gemm_mfma_default_tile(m: int, n: int, k: int) -> GemmTile:
     return t
 
 
+def launch_gemm_lp(a, b, c, ab_dtype, c_dtype, m: int, n: int, k: int, alpha: float,
+                   beta: float, tile: GemmTile | None = None, stream=None) -> Status:
+    """16-bit-input GEMM (bf16 or fp16 A and B, fp32 accumulation, C in fp32 or
+    the input type).  No reference counterpart: the reference reserves the
+    kF16/kBF16 DType tags (dtype.hpp:33-41) but launches fp32 only."""
+    tile = gemm_lp_default_tile(m, n, k) if tile is None else tile
+    return _st(lib().mcke_launch_gemm_lp(_ptr(a), _ptr(b), _ptr(c), int(ab_dtype), int(c_dtype),
+                                         m, n, k, alpha, beta, C.byref(tile), _sh(stream)))
+
+
+def gemm_lp_kernel_attrs(ab_dtype, c_dtype, tile: GemmTile):
+    """Returns (Status, KernelAttrs) of the whole-tile kernel."""
+    out = KernelAttrs()
+    st = _st(lib().mcke_gemm_lp_kernel_attrs(int(ab_dtype), int(c_dtype), C.byref(tile),
+                                             C.byref(out)))
+    return st, out
+
+
+def gemm_lp_default_tile(m: int, n: int, k: int) -> GemmTile:
+    t = GemmTile()
+    _check(lib().mcke_gemm_lp_default_tile(m, n, k, C.byref(t)))
+    return t
+
+
 # ---------------------------------------------------------------------------
 # Measured denominators (bench/fma_peak.cu, bench/stream_triad.cu counterparts)
 # ---------------------------------------------------------------------------
@@ -511,6 +546,12 @@ def launch_stream_triad_f32(b, c, a, scalar: float, n: int, stream=None) -> Stat
     return _st(lib().mcke_launch_stream_triad_f32(_ptr(b), _ptr(c), _ptr(a), scalar, n,
                                                   _sh(stream)))
 
+
+LP_TILES = (                             # the 16-bit GEMM's instantiated tiles
+    GemmTile(256, 256, 64, 16, 16),
+    GemmTile(128, 128, 64, 8, 8),
+    GemmTile(64, 64, 64, 4, 4),
+)
 
 MFMA_TILES = (
     GemmTile(256, 256, 32, 16, 16),

@@ -149,6 +149,11 @@ def lib() -> C.CDLL:
         L.orc_online_update.argtypes = [C.c_float, C.c_float, C.c_float, fp, fp]
         L.orc_online_combine.argtypes = [C.c_float, C.c_float, C.c_float, C.c_float, fp, fp]
         L.orc_online_identity_m.restype = C.c_float
+        u16 = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+        for name in ("orc_f32_to_bf16", "orc_f32_to_f16"):
+            getattr(L, name).argtypes = [_F32P, u16, C.c_size_t]
+        for name in ("orc_bf16_to_f32", "orc_f16_to_f32"):
+            getattr(L, name).argtypes = [u16, _F32P, C.c_size_t]
         _lib = L
     return _lib
 
@@ -279,6 +284,41 @@ def online_combine(a, b):
 
 def online_identity():
     return float(lib().orc_online_identity_m()), 0.0
+
+
+# ---------------------------------------------------------------------------
+# 16-bit storage formats and the 16-bit-input GEMM
+# ---------------------------------------------------------------------------
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2      # dtype.hpp:33-41
+
+
+def to_16(x, dtype: int) -> np.ndarray:
+    """float32 -> uint16 bit patterns of bf16 or fp16, rounded to nearest even."""
+    x = _f32(x)
+    out = np.empty(x.shape, dtype=np.uint16)
+    fn = lib().orc_f32_to_bf16 if dtype == DTYPE_BF16 else lib().orc_f32_to_f16
+    fn(x.ravel(), out.ravel(), x.size)
+    return out
+
+
+def from_16(h, dtype: int) -> np.ndarray:
+    """uint16 bit patterns of bf16 or fp16 -> float32 (exact)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    fn = lib().orc_bf16_to_f32 if dtype == DTYPE_BF16 else lib().orc_f16_to_f32
+    fn(h.ravel(), out.ravel(), h.size)
+    return out
+
+
+def gemm_lp(a16, b16, c, m, n, k, alpha, beta, ab_dtype: int, c_dtype: int) -> np.ndarray:
+    """The reference GEMM (double accumulation, reference.hpp:199-211) over the
+    decoded 16-bit inputs; C is read and returned in c_dtype (float32 array for
+    DTYPE_F32, else uint16 bit patterns, rounded to nearest even from the float
+    result)."""
+    af, bf = from_16(a16, ab_dtype), from_16(b16, ab_dtype)
+    cf = _f32(c) if c_dtype == DTYPE_F32 else from_16(c, c_dtype)
+    out = gemm(af, bf, cf, m, n, k, alpha, beta)
+    return out if c_dtype == DTYPE_F32 else to_16(out, c_dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -34,6 +34,15 @@
  *                        bit-equality of the sample stream with oracle/_ref.
  *   orc_online_*         identity/associativity/commutativity properties and
  *                        equality with oracle/_ref's online_update/online_combine.
+ *   orc_f32_to_bf16,     no reference counterpart (the reference reserves the 16-bit
+ *   orc_bf16_to_f32      DType tags only).  Bit-equality with torch's CPU bfloat16
+ *                        conversions on every 16-bit pattern and on 10^6 floats
+ *                        with ties, overflow, subnormals, signed zeros and NaN,
+ *                        plus hand values (1.0 -> 0x3F80, tie 1+2^-8 -> 0x3F80).
+ *   orc_f32_to_f16,      no reference counterpart.  Bit-equality with numpy's
+ *   orc_f16_to_f32       float16 conversions on every 16-bit pattern and the same
+ *                        float set, plus hand values (65504, 65520 -> inf, 2^-24,
+ *                        2^-25 -> 0).
  */
 #include <float.h>
 #include <math.h>
@@ -377,3 +386,88 @@ ORC_API void orc_online_combine(float am, float ad, float bm, float bd, float* o
 }
 
 ORC_API float orc_online_identity_m(void) { return -FLT_MAX; }
+
+/* ------------------------------------------------------------------------- */
+/* 16-bit storage formats for the 16-bit-input GEMM.  The reference has no     */
+/* conversion code (its DType reserves kF16 / kBF16, dtype.hpp:33-41, and      */
+/* dtype_size gives 2 bytes for both, :43-52); these restate IEEE 754-2008      */
+/* binary16 and the bfloat16 format (binary32 with the low 16 fraction bits    */
+/* dropped), each with round-to-nearest-even on the narrowing conversion.      */
+/* NaN stays NaN (quiet bit set, sign kept), overflow rounds to infinity.       */
+/* ------------------------------------------------------------------------- */
+static uint32_t f32_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+static float bits_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = f32_bits(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  /* Add half an ulp of the 16-bit result, plus one more when the kept part is
+   * odd, so exact ties go to the even neighbour; a carry moves into the
+   * exponent (and the largest finite values round to infinity). */
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static uint16_t f32_to_f16_rne(float f) {
+  const uint32_t u = f32_bits(f);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  if (a == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
+  const int e = (int)(a >> 23) - 127;          /* unbiased exponent (-127 for zero/denormal) */
+  const uint32_t frac = a & 0x7fffffu;
+  if (e > 15) return (uint16_t)(sign | 0x7c00u);
+  if (e >= -14) {
+    /* Normal binary16: keep 10 of 23 fraction bits, round on the 13 dropped. */
+    uint32_t h = ((uint32_t)(e + 15) << 10) | (frac >> 13);
+    const uint32_t rest = frac & 0x1fffu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h += 1u;   /* may carry to 0x7c00 = inf */
+    return (uint16_t)(sign | h);
+  }
+  /* Subnormal binary16: units of 2^-24.  The value is sig * 2^(e-23) with the
+   * 24-bit significand sig, i.e. sig >> (-e-1) units; below 2^-25 it rounds to 0
+   * (2^-25 itself is a tie that goes to the even 0). */
+  if (e < -25) return sign;
+  const uint32_t sig = frac | 0x800000u;
+  const int s = -e - 1;                         /* 14 .. 24 */
+  uint32_t q = sig >> s;
+  const uint32_t rest = sig & ((1u << s) - 1u), half = 1u << (s - 1);
+  if (rest > half || (rest == half && (q & 1u))) q += 1u;   /* 0x400 = smallest normal */
+  return (uint16_t)(sign | q);
+}
+
+static float f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0x1fu) return bits_f32(sign | 0x7f800000u | (m << 13));
+  if (e == 0) {
+    const float v = ldexpf((float)m, -24);     /* exact: m < 2^10 */
+    return sign ? -v : v;
+  }
+  return bits_f32(sign | ((e + 112u) << 23) | (m << 13));   /* rebias 15 -> 127 */
+}
+
+ORC_API void orc_f32_to_bf16(const float* x, uint16_t* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = f32_to_bf16_rne(x[i]);
+}
+
+ORC_API void orc_bf16_to_f32(const uint16_t* x, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = bits_f32((uint32_t)x[i] << 16);
+}
+
+ORC_API void orc_f32_to_f16(const float* x, uint16_t* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = f32_to_f16_rne(x[i]);
+}
+
+ORC_API void orc_f16_to_f32(const uint16_t* x, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = f16_to_f32(x[i]);
+}

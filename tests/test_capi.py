@@ -83,6 +83,8 @@ def test_enum_values_match_reference(mcke):
     assert (V.kNaive, V.kTiledSmem, V.kTiledRegBlock, V.kWarpTile, V.kCublasRef,
             V.kWarpTileNoDbuf, V.kWarpTileVec4, V.kNaiveUncoalesced, V.kMfmaF32) == tuple(range(9))
     assert [int(c) for c in mcke.StatusCode] == list(range(7))
+    # DType, include/mcke/core/dtype.hpp:33-41: kF32, kF16, kBF16 first.
+    assert (int(mcke.DType.kF32), int(mcke.DType.kF16), int(mcke.DType.kBF16)) == (0, 1, 2)
 
 
 def test_host_generators_match_oracle(mcke, orc):
@@ -213,3 +215,32 @@ def test_gemm_rejections(cpu_only):
     assert m.launch_gemm_f32(X, B, Y, 8, 8, 8, 1, 0, 42, good).code == IA
     # the ladder's 2-D grid caps the row tiles at 65535
     assert m.launch_gemm_f32(X, B, Y, 65536 * 4 + 1, 8, 8, 1, 0, V.kNaive, T()).code == IA
+
+
+def test_default_lp_tile(mcke):
+    assert mcke.gemm_lp_default_tile(8192, 8192, 8192).astuple() == (256, 256, 64, 16, 16)
+    assert mcke.gemm_lp_default_tile(4096, 4096, 4096).astuple() == (128, 128, 64, 8, 8)
+    assert mcke.gemm_lp_default_tile(1024, 1024, 1024).astuple() == (64, 64, 64, 4, 4)
+
+
+def test_gemm_lp_rejections(cpu_only):
+    m = cpu_only
+    IA = m.StatusCode.kInvalidArgument
+    D, T = m.DType, m.GemmTile
+    good = m.LP_TILES[0]
+    bf, f16, f32 = D.kBF16, D.kF16, D.kF32
+    assert m.launch_gemm_lp(X, B, Y, bf, f32, 0, 8, 8, 1, 0, good).ok()              # m == 0
+    assert m.launch_gemm_lp(None, None, None, bf, bf, 8, 0, 8, 1, 0, good).ok()      # n == 0
+    assert m.launch_gemm_lp(X, B, X, bf, f32, 8, 8, 8, 1, 0, good).code == IA        # a == c
+    assert m.launch_gemm_lp(X, B, B, f16, f16, 8, 8, 8, 1, 0, good).code == IA       # b == c
+    assert m.launch_gemm_lp(X, B, Y, bf, f32, -8, 8, 8, 1, 0, good).code == IA
+    assert m.launch_gemm_lp(X, None, Y, bf, f32, 8, 8, 8, 1, 0, good).code == IA
+    assert m.launch_gemm_lp(X, B, Y, bf, f32, 8, 8, 1 << 31, 1, 0, good).code == IA
+    st = m.launch_gemm_lp(X, B, Y, f32, f32, 8, 8, 8, 1, 0, good)                    # fp32 in
+    assert st.code == IA and "ab_dtype" in st.message
+    st = m.launch_gemm_lp(X, B, Y, bf, f16, 8, 8, 8, 1, 0, good)                     # mixed out
+    assert st.code == IA and "c_dtype" in st.message
+    st = m.launch_gemm_lp(X, B, Y, bf, f32, 8, 8, 8, 1, 0, T(256, 256, 32, 16, 16))  # fp32 tile
+    assert st.code == IA and "no fallback" in st.message
+    st, _ = m.gemm_lp_kernel_attrs(f16, f32, T(128, 128, 8, 8, 8))
+    assert st.code == IA
