@@ -261,6 +261,13 @@ int mcke_launch_mfma_peak_f32(const float* seed, float* out, int64_t blocks, int
                               void* stream);
 int mcke_launch_stream_triad_f32(const float* b, const float* c, float* a, float scalar, int64_t n,
                                  void* stream);
+/* The 16-bit MFMA counterpart of mfma_peak (no reference counterpart: the
+ * ceiling of mcke_launch_gemm_lp): the same 4 chains per wave of
+ * v_mfma_f32_32x32x16_{bf16,f16} (ab_dtype MCKE_DTYPE_BF16 or MCKE_DTYPE_F16),
+ * 32768 flops each. */
+uint64_t mcke_mfma_peak_lp_flops(int64_t blocks, int64_t iters);
+int mcke_launch_mfma_peak_lp(int ab_dtype, const float* seed, float* out, int64_t blocks,
+                             int64_t iters, void* stream);
 
 /* ---- host data generators (bench / test inputs) ----------------------------
  * The same map as the reference's fill_random (tests/reference.hpp:101-109):

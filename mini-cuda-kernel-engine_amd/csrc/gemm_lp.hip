@@ -17,8 +17,24 @@ namespace {
 
 using LpKernel = const void*;
 
+// LDS stages of the direct-to-LDS kernel per tile (32 KiB per stage at 256 x 256).
+template <int BM, int BN> struct LpDmaStages { static constexpr int value = 4; };
+
 template <typename T, typename OutT, int BM, int BN>
 struct LpTile {
+  // Whole tiles with 16-byte aligned operands take the direct-to-LDS kernel (tiles
+  // with BN >= 128), whose per-lane source offsets are 32-bit: BM rows of A and 32
+  // rows of B must span less than 4 GiB.
+  static bool use_dma(bool vec, int m, int n, int k) {
+    if constexpr (BN < 128) {
+      return false;
+    } else {
+      return vec && m % BM == 0 && n % BN == 0 && k % LpDmaShape<BM, BN, 4>::BK == 0 &&
+             static_cast<int64_t>(BM) * k * 2 < (int64_t{1} << 32) &&
+             static_cast<int64_t>(32) * n * 2 < (int64_t{1} << 32);
+    }
+  }
+
   static int launch(const void* a, const void* b, void* c, int m, int n, int k, float alpha,
                     float beta, bool vec, hipStream_t s) {
     const int64_t tiles_m = (static_cast<int64_t>(m) + BM - 1) / BM;
@@ -31,6 +47,14 @@ struct LpTile {
     auto* C = static_cast<OutT*>(c);
     const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n)), block(kMfmaThreads);
     const int tmi = static_cast<int>(tiles_m), tni = static_cast<int>(tiles_n);
+    if constexpr (BN >= 128) {
+      if (use_dma(vec, m, n, k)) {
+        gemm_lp_dma_kernel<T, OutT, BM, BN, LpDmaStages<BM, BN>::value>
+            <<<grid, block, 0, s>>>(A, B, C, m, n, k, alpha, beta, tmi, tni);
+        MCKE_LAUNCH_CHECK("gemm_lp_dma_kernel");
+        return ok();
+      }
+    }
     if (even)
       gemm_lp_kernel<T, OutT, BM, BN, true, true>
           <<<grid, block, 0, s>>>(A, B, C, m, n, k, alpha, beta, tmi, tni);
@@ -45,7 +69,12 @@ struct LpTile {
   }
   // The instantiation whole-tile shapes run, for attribute queries.
   static LpKernel kernel() {
-    return reinterpret_cast<LpKernel>(&gemm_lp_kernel<T, OutT, BM, BN, true, true>);
+    using Fn = void (*)(const uint16_t*, const uint16_t*, OutT*, int, int, int, float, float, int,
+                        int);
+    Fn fn;
+    if constexpr (BN >= 128) fn = &gemm_lp_dma_kernel<T, OutT, BM, BN, LpDmaStages<BM, BN>::value>;
+    else fn = &gemm_lp_kernel<T, OutT, BM, BN, true, true>;
+    return reinterpret_cast<LpKernel>(fn);
   }
 };
 
@@ -173,9 +202,10 @@ int mcke_gemm_lp_kernel_attrs(int ab_dtype, int c_dtype, const mcke_gemm_tile* t
 int mcke_gemm_lp_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile* out) {
   if (!out) return invalid("gemm_lp_default_tile: null out");
   (void)k;
-  // As for the fp32 MFMA kernel: the largest tile that still gives a 256-CU part
-  // four rounds of workgroups.
-  const int64_t want = 4 * 256;
+  // The largest tile that still gives every CU of a 256-CU part a workgroup:
+  // measured on MI355X, 256 x 256 wins at 4096^3 (256 tiles) and 128 x 128 at
+  // 2048^3 (256 tiles), each over the next smaller tile with more rounds.
+  const int64_t want = 256;
   auto tiles = [&](int64_t t) { return ((m + t - 1) / t) * ((n + t - 1) / t); };
   if (tiles(256) >= want) *out = mcke_gemm_tile{256, 256, kLpBK, 16, 16};
   else if (tiles(128) >= want) *out = mcke_gemm_tile{128, 128, kLpBK, 8, 8};

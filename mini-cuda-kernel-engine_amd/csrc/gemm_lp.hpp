@@ -39,6 +39,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <utility>
 
 #include "gemm_mfma.hpp"
 
@@ -354,6 +355,356 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_kernel(
   }
 
   lp_store_c<OutT, BM, BN, VEC>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
+}
+
+// ---------------------------------------------------------------------------
+// Whole-tile kernel (M % BM == N % BN == K % 32 == 0, 16-byte aligned operands):
+// both operands go straight from global memory into LDS (global_load_lds_dwordx4:
+// one instruction writes its 64 lanes' 16 bytes to 1 KB of contiguous LDS, lane j
+// at byte 16 j), STAGES deep, and B is read back transposed by the LDS
+// (ds_read_b64_tr_b16), so no operand passes through VGPRs or ds_writes.
+//
+// ds_read_b64_tr_b16, per 16-lane group: lane r supplies the address of four
+// consecutive 16-bit values R[r][0..3]; lane 4a + b receives
+// { R[a][b], R[4+a][b], R[8+a][b], R[12+a][b] }.  With lane 4j + a pointing at
+// B[k0 + j][n0 + 4a .. n0 + 4a + 3], lane 4a + b receives column n0 + 4a + b at
+// rows k0 .. k0 + 3: a k-contiguous MFMA B fragment, four values per read, two
+// reads per MFMA.  The 16 lanes of a group are the 16 consecutive columns
+// n0 .. n0 + 15, so here B fragments use the plain column order (lane c of an
+// n-tile is column c).
+//
+// K is staged 32 deep: sub-step s (0, 1) of a stage covers k = 16 s .. 16 s + 15,
+// lane half h the eight k = 16 s + 8 h + e (e = 0..7) -- one 16-byte chunk of an
+// A row, two transposed reads (e = 4 t + j, t = 0, 1) of B.
+//
+// LDS layouts (per stage; XOR swizzles keep every access conflict-free):
+//   A: BM rows of 64 bytes (4 chunks); chunk q of row r sits at position
+//      q ^ ((r / 4) % 4).  A fragment read covers 32 consecutive rows at one
+//      chunk; any 16 of them hit 16 distinct 16-byte bank groups.
+//   B: 32 rows (k) of BN * 2 bytes, n contiguous; 16-byte chunk c of row k sits
+//      at position c ^ (4 (k % 4)).  A transposed read touches rows
+//      k0 .. k0 + 3 (k0 % 4 == 0) and, per lane half, 32 consecutive columns
+//      (4 chunks): the swizzle puts the four rows' chunk quads on distinct
+//      64-byte bank groups.
+// The DMA source of each lane is chosen so that it lands on these positions.
+//
+// Pipeline: the barrier that publishes stage ks + 1 sits between the two
+// sub-steps of stage ks, so the first fragment reads of stage ks + 1 and the
+// DMA of stage ks + STAGES - 1 are issued under the MFMAs of stage ks's second
+// sub-step, and no fragment read is exposed at a barrier.
+// ---------------------------------------------------------------------------
+// Fragment reads are issued as inline asm and waited on explicitly: the
+// compiler cannot tell that a read of stage ks is disjoint from the DMA still
+// landing in other stages, and would otherwise drain every outstanding load
+// (vmcnt(0)) in front of it.  Nothing else in the kernel reads LDS, so the
+// compiler tracks no LDS read of its own, and lds_wait() is the only wait the
+// fragments need: it waits for every read issued so far and re-defines the
+// fragment registers after the wait, so no MFMA that uses them can be scheduled
+// above it.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  // A C-style cast is the address-space cast from the generic pointer.
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) char*)(p)));
+}
+
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_read128(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr16(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
+template <int MT, int NT>
+__device__ __forceinline__ void lds_wait(u32x4 (&av)[MT], u32x2 (&bv)[NT][2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < MT; ++i) asm volatile("" : "+v"(av[i]));
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    asm volatile("" : "+v"(bv[j][0]));
+    asm volatile("" : "+v"(bv[j][1]));
+  }
+}
+
+template <int BM, int BN, int STAGES>
+struct LpDmaShape {
+  static constexpr int BK = 32;
+  static constexpr int kARow = BK * 2;                    // 64 bytes
+  static constexpr int kBRow = BN * 2;                    // 256 or 512 bytes
+  static constexpr int kABytes = BM * kARow;
+  static constexpr int kBBytes = BK * kBRow;
+  static constexpr int kStageBytes = kABytes + kBBytes;
+  static constexpr int NA = kABytes / 1024 / 4;          // DMA instructions per wave per stage
+  static constexpr int NB = kBBytes / 1024 / 4;
+  static constexpr int L = NA + NB;
+  static constexpr int kBChunksPerRow = BN / 8;
+  static constexpr int kBRowsPerChunk = 1024 / kBRow;
+  static constexpr int MT = BM / 64, NT = BN / 64;       // MFMA tiles per wave
+  static constexpr int kMfmas = MT * NT;                 // per sub-step
+  static constexpr int kReads = MT + 2 * NT;             // fragment reads per sub-step
+  static_assert(BN == 128 || BN == 256, "B rows of 16 or 32 chunks");
+  static_assert(kABytes % 4096 == 0 && kBBytes % 4096 == 0, "stage must split over 4 waves");
+  static_assert(STAGES >= 3 && (STAGES - 2) * L <= 63, "vmcnt counts at most 63 loads");
+  static_assert(STAGES * kStageBytes <= 160 * 1024, "LDS holds 160 KiB");
+  static_assert((16 + 4) * kBRow + 4 * 32 * kARow < 65536, "ds offsets are 16-bit");
+
+  // Issues DMA instruction ii (A chunks first, then B) of this wave's share of
+  // K step `kstep` into the stage at `stage`.
+  static __device__ __forceinline__ void issue_dma(int ii, const char* a_base, const char* b_base,
+                                                   int64_t b_step, const uint32_t (&a_src)[NA],
+                                                   const uint32_t (&b_src)[NB], int kstep,
+                                                   char* stage, int wave) {
+    if (ii < NA) {
+      __builtin_amdgcn_global_load_lds(a_base + static_cast<int64_t>(kstep) * (BK * 2) + a_src[ii],
+                                       stage + (wave * NA + ii) * 1024, 16, 0, 0);
+    } else {
+      const int ib = ii - NA;
+      __builtin_amdgcn_global_load_lds(b_base + kstep * b_step + b_src[ib],
+                                       stage + kABytes + (wave * NB + ib) * 1024, 16, 0, 0);
+    }
+  }
+
+  // Fragment read rr of sub-step S of the stage at LDS address `st`: rr < MT
+  // reads A for m-tile rr, then B for n-tile (rr - MT) / 2, transposed read t =
+  // (rr - MT) % 2.
+  template <int SUB, int RR>
+  static __device__ __forceinline__ void read_one(uint32_t st, const uint32_t (&a_off)[2],
+                                                  const uint32_t (&b_off)[NT], u32x4 (&av)[MT],
+                                                  u32x2 (&bv)[NT][2]) {
+    if constexpr (RR < MT) {
+      av[RR] = lds_read128<RR * 32 * kARow>(st + a_off[SUB]);
+    } else {
+      constexpr int jn = (RR - MT) / 2, t = (RR - MT) % 2;
+      bv[jn][t] = lds_read_tr16<(16 * SUB + 4 * t) * kBRow>(st + b_off[jn]);
+    }
+  }
+};
+
+// Sub-step helper: MFMA idx of the MT x NT grid, then whichever fragment reads
+// (of sub-step SUB of the stage at `st`) and DMA instructions fall in its slot,
+// so that they issue while the matrix pipe is busy.
+template <typename T, int BM, int BN, int STAGES, int SUB, int IDX>
+__device__ __forceinline__ void lp_dma_slot(f32x16 (&acc)[BM / 64][BN / 64],
+                                            const u32x4 (&cav)[BM / 64],
+                                            const u32x2 (&cbv)[BN / 64][2], uint32_t st,
+                                            const uint32_t (&a_off)[2],
+                                            const uint32_t (&b_off)[BN / 64],
+                                            u32x4 (&nav)[BM / 64], u32x2 (&nbv)[BN / 64][2],
+                                            bool dma, const char* a_base, const char* b_base,
+                                            int64_t b_step, const uint32_t (&a_src)[LpDmaShape<BM, BN, STAGES>::NA],
+                                            const uint32_t (&b_src)[LpDmaShape<BM, BN, STAGES>::NB],
+                                            int kstep, char* dstage, int wave) {
+  using S = LpDmaShape<BM, BN, STAGES>;
+  constexpr int i = IDX / S::NT, j = IDX % S::NT;
+  const u32x4 b = u32x4{cbv[j][0][0], cbv[j][0][1], cbv[j][1][0], cbv[j][1][1]};
+  acc[i][j] = LpMfma<T>::run(cav[i], b, acc[i][j]);
+  __builtin_amdgcn_sched_barrier(0);
+  // Reads RR with RR * kMfmas / kReads == IDX go after this MFMA.
+  [&]<int... RR>(std::integer_sequence<int, RR...>) {
+    ((RR * S::kMfmas / S::kReads == IDX
+          ? S::template read_one<SUB, RR>(st, a_off, b_off, nav, nbv)
+          : void()),
+     ...);
+  }(std::make_integer_sequence<int, S::kReads>{});
+  if (dma) {
+#pragma unroll
+    for (int ii = 0; ii < S::L; ++ii)
+      if (ii * S::kMfmas / S::L == IDX)
+        S::issue_dma(ii, a_base, b_base, b_step, a_src, b_src, kstep, dstage, wave);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// ---------------------------------------------------------------------------
+// Whole-tile kernel (M % BM == N % BN == K % 32 == 0, 16-byte aligned operands):
+// both operands go straight from global memory into LDS (global_load_lds_dwordx4:
+// one instruction writes its 64 lanes' 16 bytes to 1 KB of contiguous LDS, lane j
+// at byte 16 j), STAGES deep, and B is read back transposed by the LDS
+// (ds_read_b64_tr_b16), so no operand passes through VGPRs or ds_writes.
+//
+// ds_read_b64_tr_b16, per 16-lane group: lane r supplies the address of four
+// consecutive 16-bit values R[r][0..3]; lane 4a + b receives
+// { R[a][b], R[4+a][b], R[8+a][b], R[12+a][b] }.  With lane 4j + a pointing at
+// B[k0 + j][n0 + 4a .. n0 + 4a + 3], lane 4a + b receives column n0 + 4a + b at
+// rows k0 .. k0 + 3: a k-contiguous MFMA B fragment, four values per read, two
+// reads per MFMA.  The 16 lanes of a group are the 16 consecutive columns
+// n0 .. n0 + 15, so here B fragments use the plain column order (lane c of an
+// n-tile is column c).
+//
+// K is staged 32 deep: sub-step s (0, 1) of a stage covers k = 16 s .. 16 s + 15,
+// lane half h the eight k = 16 s + 8 h + e (e = 0..7) -- one 16-byte chunk of an
+// A row, two transposed reads (e = 4 t + j, t = 0, 1) of B.
+//
+// LDS layouts (per stage; XOR swizzles keep every access conflict-free):
+//   A: BM rows of 64 bytes (4 chunks); chunk q of row r sits at position
+//      q ^ ((r / 4) % 4).  A fragment read covers 32 consecutive rows at one
+//      chunk; any 16 of them hit 16 distinct 16-byte bank groups.
+//   B: 32 rows (k) of BN * 2 bytes, n contiguous; 16-byte chunk c of row k sits
+//      at position c ^ (4 (k % 4)).  A transposed read touches rows
+//      k0 .. k0 + 3 (k0 % 4 == 0) and, per lane half, 32 consecutive columns
+//      (4 chunks): the swizzle puts the four rows' chunk quads on distinct
+//      64-byte bank groups.
+// The DMA source of each lane is chosen so that it lands on these positions.
+//
+// Pipeline, per stage ks:
+//   sub-step 0: MFMAs on fragments read earlier, interleaved with the reads of
+//               sub-step 1;
+//   barrier:    publishes stage ks + 1 (its DMA was issued STAGES - 2 stages
+//               earlier) and retires every read of stage ks - 1's buffer;
+//   sub-step 1: MFMAs interleaved with the DMA of stage ks + STAGES - 1 (into
+//               stage ks - 1's buffer) and the sub-step 0 reads of stage ks + 1.
+// ---------------------------------------------------------------------------
+template <typename T, typename OutT, int BM, int BN, int STAGES>
+__global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, OutT* __restrict__ C,
+    int M, int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
+  using S = LpDmaShape<BM, BN, STAGES>;
+  constexpr int BK = S::BK;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MT = S::MT, NT = S::NT;
+  constexpr int L = S::L;
+
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * S::kStageBytes];
+
+  int tm, tn;
+  mfma_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int wm = wave / 2, wn = wave % 2;
+  const int h = lane / 32, c = lane % 32;
+
+  // DMA sources: a wave-uniform base per stage plus a per-lane byte offset.
+  const char* a_base = reinterpret_cast<const char*>(A + static_cast<int64_t>(m0) * K);
+  const char* b_base = reinterpret_cast<const char*>(B + n0);
+  const int64_t b_step = static_cast<int64_t>(BK) * N * 2;        // bytes per stage
+  uint32_t a_src[S::NA], b_src[S::NB];
+#pragma unroll
+  for (int ii = 0; ii < S::NA; ++ii) {
+    const int row = 16 * (wave * S::NA + ii) + lane / 4;       // (row / 4) % 4 == lane / 16
+    const int q = (lane % 4) ^ (lane / 16);
+    a_src[ii] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) * 2u + 16u * q;
+  }
+#pragma unroll
+  for (int ii = 0; ii < S::NB; ++ii) {
+    const int row = S::kBRowsPerChunk * (wave * S::NB + ii) + lane / S::kBChunksPerRow;
+    const int cg = (lane % S::kBChunksPerRow) ^ (4 * (row % 4));
+    b_src[ii] = static_cast<uint32_t>(row) * static_cast<uint32_t>(N) * 2u + 16u * cg;
+  }
+
+  // Fragment addressing (bytes within a stage).
+  //   A, m-tile i, sub-step s: row wm*WM + 32 i + c, chunk 2 s + h at position
+  //   (2 s + h) ^ ((c / 4) % 4)   (the row base is a multiple of 32).
+  uint32_t a_off[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+    a_off[s] = (wm * WM + c) * S::kARow + 16 * ((2 * s + h) ^ ((c / 4) % 4));
+  //   B, n-tile jn, sub-step s, read t: lane r = 4 jq + a of its 16-lane group g
+  //   reads row k = 16 s + 8 h + 4 t + jq at columns wn*WN + 32 jn + 16 (g % 2) + 4 a.
+  const int r16 = lane % 16, jq = r16 / 4, qa = r16 % 4, g2 = (lane / 16) % 2;
+  uint32_t b_off[NT];
+#pragma unroll
+  for (int jn = 0; jn < NT; ++jn) {
+    const int cc = (wn * WN + 32 * jn + 16 * g2 + 4 * qa) / 8;
+    b_off[jn] = S::kABytes + (8 * h + jq) * S::kBRow + 16 * (cc ^ (4 * jq)) + (qa % 2) * 8;
+  }
+
+  f32x16 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const uint32_t lds0 = lds_addr(smem);
+  const int ksteps = K / BK;
+  u32x4 av0[MT], av1[MT];
+  u32x2 bv0[NT][2], bv1[NT][2];
+  if (ksteps > 0) {
+    // Prologue: stages 0 .. STAGES-2 in flight (past the last K step a stage
+    // re-fetches the last one into a buffer nobody reads, which keeps the number
+    // of loads per stage -- and so the vmcnt arithmetic -- uniform).
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+#pragma unroll
+      for (int ii = 0; ii < L; ++ii)
+        S::issue_dma(ii, a_base, b_base, b_step, a_src, b_src, st < ksteps ? st : ksteps - 1,
+                     smem + st * S::kStageBytes, wave);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - 2) * L) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    [&]<int... RR>(std::integer_sequence<int, RR...>) {
+      (S::template read_one<0, RR>(lds0, a_off, b_off, av0, bv0), ...);
+    }(std::make_integer_sequence<int, S::kReads>{});
+  }
+
+  for (int ks = 0; ks < ksteps; ++ks) {
+    const uint32_t st = lds0 + (ks % STAGES) * S::kStageBytes;
+    const uint32_t st_next = lds0 + ((ks + 1) % STAGES) * S::kStageBytes;
+    const int kf = ks + STAGES - 1;
+    const int kdma = kf < ksteps ? kf : ksteps - 1;
+    char* dstage = smem + (kf % STAGES) * S::kStageBytes;
+
+    // Sub-step 0 (fragments read in the previous step or the prologue).
+    lds_wait<MT, NT>(av0, bv0);
+    __builtin_amdgcn_sched_barrier(0);
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      (lp_dma_slot<T, BM, BN, STAGES, 1, I>(acc, av0, bv0, st, a_off, b_off, av1, bv1, false,
+                                            a_base, b_base, b_step, a_src, b_src, kdma, dstage,
+                                            wave),
+       ...);
+    }(std::make_integer_sequence<int, S::kMfmas>{});
+
+    // Stage ks + 1 has landed once at most the (STAGES - 3) younger stages' loads
+    // are outstanding; the barrier publishes every wave's share of it, and it also
+    // retires every wave's reads of the buffer refilled next (stage ks - 1's,
+    // waited for by lds_wait before its last MFMAs).  A bare s_barrier:
+    // __syncthreads() would drain every outstanding load (vmcnt(0)).
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - 3) * L) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Sub-step 1, with the DMA of stage ks + STAGES - 1 and the sub-step 0 reads of
+    // stage ks + 1 (in the last step they read a buffer nobody uses: harmless).
+    lds_wait<MT, NT>(av1, bv1);
+    __builtin_amdgcn_sched_barrier(0);
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      (lp_dma_slot<T, BM, BN, STAGES, 0, I>(acc, av1, bv1, st_next, a_off, b_off, av0, bv0,
+                                            true, a_base, b_base, b_step, a_src, b_src, kdma,
+                                            dstage, wave),
+       ...);
+    }(std::make_integer_sequence<int, S::kMfmas>{});
+  }
+  // No LDS DMA may still be landing, and no LDS read outstanding, when the
+  // workgroup retires.
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+
+  // Epilogue: lane (h, c) of n-tile jn holds column wn*WN + 32 jn + c.
+  using O = LpOut<OutT>;
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+      OutT* crow = C + static_cast<int64_t>(row) * N + n0 + wn * WN + c;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        float v = alpha * acc[i][j][r];
+        if (beta != 0.0f) v += beta * O::to_f32(crow[32 * j]);
+        crow[32 * j] = O::from_f32(v);
+      }
+    }
+  }
 }
 
 }  // namespace mcke_amd

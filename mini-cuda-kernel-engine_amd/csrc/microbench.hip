@@ -17,11 +17,10 @@
 
 #include "common.hpp"
 #include "device_math.hpp"
+#include "gemm_lp.hpp"
 
 namespace mcke_amd {
 namespace {
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPeakThreads = 256;   // 4 waves per workgroup
 constexpr int kChains = 4;          // independent accumulators per wave
@@ -41,6 +40,41 @@ __global__ __launch_bounds__(kPeakThreads) void mfma_peak_f32_kernel(const float
   for (int64_t i = 0; i < iters; ++i) {
 #pragma unroll
     for (int c = 0; c < kChains; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[c], 0, 0, 0);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kChains; ++c) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += acc[c][r];
+  }
+  out[static_cast<int64_t>(blockIdx.x) * kPeakThreads + threadIdx.x] = s;
+}
+
+// The same four chains on the 16-bit MFMA (v_mfma_f32_32x32x16_{bf16,f16}),
+// the ceiling of the 16-bit-input GEMM.  Operands are the seeds rounded to T.
+constexpr uint64_t kFlopsPerMfmaLp = 2ull * 32 * 32 * 16;
+
+template <typename T>
+__global__ __launch_bounds__(kPeakThreads) void mfma_peak_lp_kernel(const float* __restrict__ seed,
+                                                                    float* __restrict__ out,
+                                                                    int64_t iters) {
+  T av[8], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    av[e] = static_cast<T>(seed[(threadIdx.x + e) % kPeakThreads]);
+    bv[e] = static_cast<T>(seed[(threadIdx.x + 8 + e) % kPeakThreads]);
+  }
+  const u32x4 a = __builtin_bit_cast(u32x4, av);
+  const u32x4 b = __builtin_bit_cast(u32x4, bv);
+  f32x16 acc[kChains];
+#pragma unroll
+  for (int c = 0; c < kChains; ++c) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[c][r] = 0.0f;
+  }
+  for (int64_t i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int c = 0; c < kChains; ++c) acc[c] = LpMfma<T>::run(a, b, acc[c]);
   }
   float s = 0.0f;
 #pragma unroll
@@ -97,6 +131,30 @@ int mcke_launch_mfma_peak_f32(const float* seed, float* out, int64_t blocks, int
   mfma_peak_f32_kernel<<<static_cast<unsigned>(blocks), kPeakThreads, 0,
                          static_cast<hipStream_t>(stream)>>>(seed, out, iters);
   MCKE_LAUNCH_CHECK("mfma_peak_f32_kernel");
+  return ok();
+}
+
+uint64_t mcke_mfma_peak_lp_flops(int64_t blocks, int64_t iters) {
+  if (blocks <= 0 || iters <= 0) return 0;
+  return static_cast<uint64_t>(blocks) * (kPeakThreads / kWave) * static_cast<uint64_t>(iters) *
+         kChains * kFlopsPerMfmaLp;
+}
+
+int mcke_launch_mfma_peak_lp(int ab_dtype, const float* seed, float* out, int64_t blocks,
+                             int64_t iters, void* stream) {
+  if (ab_dtype != MCKE_DTYPE_BF16 && ab_dtype != MCKE_DTYPE_F16)
+    return invalid("launch_mfma_peak_lp: ab_dtype must be MCKE_DTYPE_BF16 or MCKE_DTYPE_F16");
+  if (!seed || !out) return invalid("launch_mfma_peak_lp: null pointer");
+  if (blocks <= 0 || blocks > 0x7fffffff) return invalid("launch_mfma_peak_lp: blocks out of range");
+  if (iters <= 0) return invalid("launch_mfma_peak_lp: iters must be > 0");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ab_dtype == MCKE_DTYPE_BF16)
+    mfma_peak_lp_kernel<__bf16><<<static_cast<unsigned>(blocks), kPeakThreads, 0, s>>>(seed, out,
+                                                                                       iters);
+  else
+    mfma_peak_lp_kernel<_Float16><<<static_cast<unsigned>(blocks), kPeakThreads, 0, s>>>(seed, out,
+                                                                                         iters);
+  MCKE_LAUNCH_CHECK("mfma_peak_lp_kernel");
   return ok();
 }
 

@@ -219,7 +219,8 @@ def test_gemm_rejections(cpu_only):
 
 def test_default_lp_tile(mcke):
     assert mcke.gemm_lp_default_tile(8192, 8192, 8192).astuple() == (256, 256, 64, 16, 16)
-    assert mcke.gemm_lp_default_tile(4096, 4096, 4096).astuple() == (128, 128, 64, 8, 8)
+    assert mcke.gemm_lp_default_tile(4096, 4096, 4096).astuple() == (256, 256, 64, 16, 16)
+    assert mcke.gemm_lp_default_tile(2048, 2048, 2048).astuple() == (128, 128, 64, 8, 8)
     assert mcke.gemm_lp_default_tile(1024, 1024, 1024).astuple() == (64, 64, 64, 4, 4)
 
 
