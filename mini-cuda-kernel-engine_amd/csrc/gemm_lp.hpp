@@ -373,6 +373,13 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_kernel(
 // n0 .. n0 + 15, so here B fragments use the plain column order (lane c of an
 // n-tile is column c).
 //
+// Epilogue layout.  For fp32 C, A is the MFMA's first operand: lane c of a tile
+// holds one column, and the 32 lanes of a half-wave store 128 contiguous bytes of
+// a row per instruction (whole cache lines).  For 16-bit C the operands are
+// swapped, so each MFMA accumulates a transposed 32 x 32 tile in which a lane
+// holds runs of four adjacent columns (one 8-byte store each) -- fewer, wider
+// stores than 2-byte ones, which measure faster there.
+//
 // K is staged 32 deep: sub-step s (0, 1) of a stage covers k = 16 s .. 16 s + 15,
 // lane half h the eight k = 16 s + 8 h + e (e = 0..7) -- one 16-byte chunk of an
 // A row, two transposed reads (e = 4 t + j, t = 0, 1) of B.
@@ -490,7 +497,7 @@ struct LpDmaShape {
 // Sub-step helper: MFMA idx of the MT x NT grid, then whichever fragment reads
 // (of sub-step SUB of the stage at `st`) and DMA instructions fall in its slot,
 // so that they issue while the matrix pipe is busy.
-template <typename T, int BM, int BN, int STAGES, int SUB, int IDX>
+template <typename T, bool TRANS, int BM, int BN, int STAGES, int SUB, int IDX>
 __device__ __forceinline__ void lp_dma_slot(f32x16 (&acc)[BM / 64][BN / 64],
                                             const u32x4 (&cav)[BM / 64],
                                             const u32x2 (&cbv)[BN / 64][2], uint32_t st,
@@ -504,7 +511,9 @@ __device__ __forceinline__ void lp_dma_slot(f32x16 (&acc)[BM / 64][BN / 64],
   using S = LpDmaShape<BM, BN, STAGES>;
   constexpr int i = IDX / S::NT, j = IDX % S::NT;
   const u32x4 b = u32x4{cbv[j][0][0], cbv[j][0][1], cbv[j][1][0], cbv[j][1][1]};
-  acc[i][j] = LpMfma<T>::run(cav[i], b, acc[i][j]);
+  // TRANS: operands swapped, the MFMA computes the transposed tile (n rows, m columns).
+  if constexpr (TRANS) acc[i][j] = LpMfma<T>::run(b, cav[i], acc[i][j]);
+  else acc[i][j] = LpMfma<T>::run(cav[i], b, acc[i][j]);
   __builtin_amdgcn_sched_barrier(0);
   // Reads RR with RR * kMfmas / kReads == IDX go after this MFMA.
   [&]<int... RR>(std::integer_sequence<int, RR...>) {
@@ -570,6 +579,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int MT = S::MT, NT = S::NT;
   constexpr int L = S::L;
+  constexpr bool TRANS = sizeof(OutT) == 2;
 
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * S::kStageBytes];
 
@@ -658,7 +668,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
     lds_wait<MT, NT>(av0, bv0);
     __builtin_amdgcn_sched_barrier(0);
     [&]<int... I>(std::integer_sequence<int, I...>) {
-      (lp_dma_slot<T, BM, BN, STAGES, 1, I>(acc, av0, bv0, st, a_off, b_off, av1, bv1, false,
+      (lp_dma_slot<T, TRANS, BM, BN, STAGES, 1, I>(acc, av0, bv0, st, a_off, b_off, av1, bv1, false,
                                             a_base, b_base, b_step, a_src, b_src, kdma, dstage,
                                             wave),
        ...);
@@ -679,7 +689,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
     lds_wait<MT, NT>(av1, bv1);
     __builtin_amdgcn_sched_barrier(0);
     [&]<int... I>(std::integer_sequence<int, I...>) {
-      (lp_dma_slot<T, BM, BN, STAGES, 0, I>(acc, av1, bv1, st_next, a_off, b_off, av0, bv0,
+      (lp_dma_slot<T, TRANS, BM, BN, STAGES, 0, I>(acc, av1, bv1, st_next, a_off, b_off, av0, bv0,
                                             true, a_base, b_base, b_step, a_src, b_src, kdma,
                                             dstage, wave),
        ...);
@@ -689,19 +699,49 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
   // workgroup retires.
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 
-  // Epilogue: lane (h, c) of n-tile jn holds column wn*WN + 32 jn + c.
   using O = LpOut<OutT>;
+  if constexpr (!TRANS) {
+    // Lane (h, c) of n-tile j holds column wn*WN + 32 j + c, register r row
+    // 8 (r / 4) + 4 h + r % 4 of m-tile i.
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        OutT* crow = C + static_cast<int64_t>(row) * N + n0 + wn * WN + c;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          float v = alpha * acc[i][j][r];
+          if (beta != 0.0f) v += beta * O::to_f32(crow[32 * j]);
+          crow[32 * j] = O::from_f32(v);
+        }
+      }
+    }
+    return;
+  }
+  // Transposed tiles: lane (h, c), register r = 4 g + e holds C row
+  // wm*WM + 32 i + c, column wn*WN + 32 j + 8 g + 4 h + e -- e = 0..3 are four
+  // adjacent columns, one 8-byte store.
+  struct alignas(4 * sizeof(OutT)) Quad { OutT v[4]; };
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
+    OutT* crow = C + static_cast<int64_t>(m0 + wm * WM + 32 * i + c) * N + n0 + wn * WN + 4 * h;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-      OutT* crow = C + static_cast<int64_t>(row) * N + n0 + wn * WN + c;
+    for (int j = 0; j < NT; ++j) {
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        float v = alpha * acc[i][j][r];
-        if (beta != 0.0f) v += beta * O::to_f32(crow[32 * j]);
-        crow[32 * j] = O::from_f32(v);
+      for (int g = 0; g < 4; ++g) {
+        Quad* dst = reinterpret_cast<Quad*>(crow + 32 * j + 8 * g);
+        Quad o;
+        if (beta != 0.0f) {
+          const Quad old = *dst;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o.v[e] = O::from_f32(alpha * acc[i][j][4 * g + e] + beta * O::to_f32(old.v[e]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o.v[e] = O::from_f32(alpha * acc[i][j][4 * g + e]);
+        }
+        *dst = o;
       }
     }
   }
