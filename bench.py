@@ -22,8 +22,10 @@ are included, per-launch event overhead is not.  After the timed region a
 diagnostic pass brackets single launches with their own events for median/min.
 
 Also measured in the same run: the denominators (fp32 MFMA peak sustained for
-about the GEMM's duration, a STREAM triad), the GEMM size sweep, the config-5
-graph section and the CPU baseline.
+about the GEMM's duration, a STREAM triad), the GEMM size sweep, the 16-bit-input
+GEMM (`gemm_lp`: bf16 / fp16 in, fp32 accumulation, against the published 2.5
+PFLOP/s dense peak, the measured 16-bit MFMA peak and rocBLAS on the same
+shapes), the config-5 graph section and the CPU baseline.
 
 The CPU leg (skipped with --no-cpu) checks every op's output at its timed shape
 against the CPU oracle (ops[*].parity: the GEMM by the reference's 1024-entry spot
@@ -396,6 +398,128 @@ def gemm_sweep(m, stream, iters=10):
     return out
 
 
+PEAK_16BIT_MFMA_TFLOPS = 2500.0   # MI355X dense bf16 / fp16 matrix, AMD published
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns, round to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def gemm_lp_section(m, stream, iters=10, with_peak=True):
+    """The 16-bit-input GEMM (bf16 / fp16 A and B, fp32 accumulation) at 8192^3 for
+    each output type, and bf16 -> bf16 at the sweep sizes; beside it the 16-bit
+    MFMA peak sustained for about the 8192^3 launch length and the vendor library
+    (rocBLAS gemm_ex, bf16 -> bf16) on the same shapes.  Returns (result dict,
+    verify closures for the CPU leg)."""
+    D, DT = m.DeviceBuffer, m.DType
+    runs, verifies, bufs = [], [], {}
+    traffic = profiled_traffic()
+    names = {int(DT.kBF16): "bf16", int(DT.kF16): "f16", int(DT.kF32): "f32"}
+
+    def inputs(n, ab):
+        key = (n, int(ab))
+        if key not in bufs:
+            ha = m.fill_random(n * n, 0x6E33A)
+            hb = m.fill_random(n * n, 0x8B10C)
+            if int(ab) == int(DT.kBF16):
+                ha16, hb16 = to_bf16_bits(ha), to_bf16_bits(hb)
+            else:
+                ha16 = ha.astype(np.float16).view(np.uint16)
+                hb16 = hb.astype(np.float16).view(np.uint16)
+            bufs[key] = (D.from_array(ha16), D.from_array(hb16), ha16, hb16)
+        return bufs[key]
+
+    def time_launch(fn):
+        for _ in range(3):
+            fn()
+        e0, e1 = m.Event(), m.Event()
+        e0.record(stream)
+        for _ in range(iters):
+            fn()
+        e1.record(stream)
+        stream.synchronize()
+        return e0.elapsed_ms(e1) / iters
+
+    cases = [(8192, DT.kBF16, DT.kBF16), (8192, DT.kBF16, DT.kF32), (8192, DT.kF16, DT.kF16),
+             (8192, DT.kF16, DT.kF32), (4096, DT.kBF16, DT.kBF16), (2048, DT.kBF16, DT.kBF16),
+             (1024, DT.kBF16, DT.kBF16)]
+    for n, ab, cd in cases:
+        da, db, ha16, hb16 = inputs(n, ab)
+        dc = D(n * n * (4 if int(cd) == int(DT.kF32) else 2))
+        tile = m.gemm_lp_default_tile(n, n, n)
+
+        def launch(da=da, db=db, dc=dc, n=n, ab=ab, cd=cd, tile=tile):
+            st = m.launch_gemm_lp(da, db, dc, ab, cd, n, n, n, 1.0, 0.0, tile, stream)
+            if not st.ok():
+                raise RuntimeError(str(st))
+        ms = time_launch(launch)
+        tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
+        c_bytes = 4 if int(cd) == int(DT.kF32) else 2
+        run = {"n": n, "ab": names[int(ab)], "c": names[int(cd)], "tile": tile.astuple(),
+               "avg_ms": round(ms, 5), "tflops": round(tf, 1),
+               "frac": round(tf / PEAK_16BIT_MFMA_TFLOPS, 4),
+               "algorithmic_bytes": 2 * n * n * 2 + n * n * c_bytes}
+        tr = traffic.get(f"gemm_lp_{run['ab']}_{run['c']}_{n}")
+        if tr is not None:
+            run["hbm_traffic_bytes"] = tr
+        runs.append(run)
+        log(f"gemm_lp {names[int(ab)]}->{names[int(cd)]} {n}^3: {ms:.4f} ms  {tf:.1f} TFLOP/s")
+        if n == 8192:
+            def verify(orc, run=run, dc=dc, ha16=ha16, hb16=hb16, n=n, ab=ab, cd=cd):
+                af, bf = orc.from_16(ha16, int(ab)), orc.from_16(hb16, int(ab))
+                if int(cd) == int(DT.kF32):
+                    got, extra = dc.download(n * n), 0.0
+                else:
+                    got = orc.from_16(dc.download(n * n, np.uint16), int(cd))
+                    extra = 2.0 ** -7 if int(cd) == int(DT.kBF16) else 2.0 ** -10
+                r = orc.spot_check_gemm(af, bf, got, n, n, n, 1.0, 1024, 0x5A11E,
+                                        orc.tol_gemm(n) + extra, orc.abs_tol_gemm(n))
+                run["parity"] = {"ok": r.checked == 1024 and r.mismatches == 0,
+                                 "max_abs_err": r.max_abs_err, "max_rel_err": r.max_rel_err,
+                                 "check": "1024-entry spot check in double over the decoded "
+                                          f"16-bit inputs, rel tol_gemm({n})"
+                                          + (f" + {extra:g} (output ulp)" if extra else "")
+                                          + f" + abs abs_tol_gemm({n})"}
+                return run["parity"]
+            verifies.append((f"gemm_lp {run['ab']}->{run['c']}", verify))
+
+    out = {"peak_published_tflops": PEAK_16BIT_MFMA_TFLOPS, "runs": runs}
+    if with_peak:
+        info = m.query_device(0)
+        blocks = info.sm_count * 2
+        seed = D.from_array((np.arange(256, dtype=np.float32) % 7 - 3) * 0.25)
+        sink = D(blocks * 256 * 4)
+        ms8 = next(r["avg_ms"] for r in runs if r["n"] == 8192)
+        iters_pk = max(1, int(ms8 * 1e-3 * 1.8e15 / m.mfma_peak_lp_flops(blocks, 1)))
+        for dt in (DT.kBF16, DT.kF16):
+            ms = time_launch(lambda dt=dt: m.launch_mfma_peak_lp(dt, seed, sink, blocks, iters_pk,
+                                                                 stream).throw_if_error())
+            out[f"measured_peak_{names[int(dt)]}_tflops"] = round(
+                m.mfma_peak_lp_flops(blocks, iters_pk) / (ms * 1e-3) / 1e12, 1)
+        for r in runs:
+            pk = out[f"measured_peak_{r['ab']}_tflops"]
+            r["frac_of_measured"] = round(r["tflops"] / pk, 4)
+        out["peak_note"] = (f"blocks = 2 x CUs, 4 waves each, 4 chains of "
+                            f"v_mfma_f32_32x32x16_{{bf16,f16}}, {iters_pk} iterations (~8192^3 "
+                            "launch length)")
+        log(f"measured 16-bit MFMA peak: bf16 {out['measured_peak_bf16_tflops']} TFLOP/s, "
+            f"f16 {out['measured_peak_f16_tflops']} TFLOP/s")
+    # Vendor library on the same shapes (bf16 -> bf16, rocBLAS gemm_ex), for comparison only.
+    vendor = []
+    for n in (8192, 4096, 2048, 1024):
+        da, db, _, _ = inputs(n, DT.kBF16)
+        dc = D(n * n * 2)
+        ms = time_launch(lambda da=da, db=db, dc=dc, n=n: m.launch_gemm_lp_vendor(
+            da, db, dc, DT.kBF16, DT.kBF16, n, n, n, 1.0, 0.0, stream).throw_if_error())
+        vendor.append({"n": n, "avg_ms": round(ms, 5),
+                       "tflops": round(2 * n ** 3 / (ms * 1e-3) / 1e12, 1)})
+        log(f"vendor rocBLAS gemm_ex bf16->bf16 {n}^3: {ms:.4f} ms  {vendor[-1]['tflops']} TFLOP/s")
+    out["vendor_bf16_rocblas"] = vendor
+    return out, verifies
+
+
 def graph_section(m, steps=5, warmup=2):
     """BASELINE config 5 through the GraphExecutor (buddy allocator, chain-greedy
     schedule, happens-before arena reuse):
@@ -576,6 +700,7 @@ def main(argv=None) -> int:
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-graph", action="store_true", help="skip the config-5 graph section")
     p.add_argument("--no-peaks", action="store_true", help="skip the measured-peak microbenches")
+    p.add_argument("--no-lp", action="store_true", help="skip the 16-bit-input GEMM section")
     p.add_argument("--only", default=None,
                    help="comma-separated op-name prefixes to run (profiling); enables "
                         "the copy_256mib calibration op")
@@ -596,6 +721,9 @@ def main(argv=None) -> int:
     stream = m.Stream()
     ops, keep, gemm_bufs = build_ops(m, stream, only)
 
+    if only is not None and not ops and not any(x.startswith("gemm_lp") for x in only):
+        print(f"bench.py: --only {args.only} names no op", file=sys.stderr)
+        return 2
     log(f"warmup: {args.warmup} steps")
     run_steps(m, stream, ops, args.warmup, record=False)
     log(f"timed: {args.steps} steps")
@@ -619,6 +747,9 @@ def main(argv=None) -> int:
             f"({100 * s['frac']:.1f}% of {s['peak']})")
 
     sweep = [] if (args.no_sweep or only is not None) else gemm_sweep(m, stream)
+    lp_res, lp_verify = None, []
+    if not args.no_lp and (only is None or any(x.startswith("gemm_lp") for x in only)):
+        lp_res, lp_verify = gemm_lp_section(m, stream, with_peak=not args.no_peaks)
     graph_res = None if (args.no_graph or only is not None) else graph_section(m)
     cpu = None
     if not args.no_cpu:
@@ -631,13 +762,20 @@ def main(argv=None) -> int:
                 op.parity = op.verify(oracle)
                 log(f"parity {op.name}: {'OK' if op.parity['ok'] else 'FAILED'} "
                     f"({time.perf_counter() - t0:.1f} s)")
+        for name, verify in lp_verify:
+            t0 = time.perf_counter()
+            res = verify(oracle)
+            log(f"parity {name}: {'OK' if res['ok'] else 'FAILED'} "
+                f"({time.perf_counter() - t0:.1f} s)")
     if not args.no_cpu and gemm_bufs[0] is not None:
         log(f"cpu baseline: reference GEMM on a row slab (~{args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(m, gemm_bufs, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} TFLOP/s ({cpu['sample']})")
     summaries = [op.summary(s["measured_peak"] if "measured_peak" in s else None,
                             s.get("hbm_traffic_bytes")) for op, s in zip(ops, summaries)]
-    gemm = summaries[0]
+    # A profiling run restricted by --only may hold no fp32 op at all.
+    gemm = summaries[0] if summaries else {"achieved": None, "unit": None, "bound": None,
+                                           "peak": None, "frac": None, "name": None}
 
     line = {
         "metric": METRIC,
@@ -669,6 +807,7 @@ def main(argv=None) -> int:
         "cpu_baseline": cpu,
         "ops": summaries,
         "gemm_sweep": sweep,
+        "gemm_lp": lp_res,
         "graph": graph_res,
     }
     print(json.dumps(line), flush=True)

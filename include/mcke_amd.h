@@ -197,6 +197,13 @@ int mcke_gemm_lp_kernel_attrs(int ab_dtype, int c_dtype, const mcke_gemm_tile* t
 /* The tile this build picks for a 16-bit GEMM of this shape. */
 int mcke_gemm_lp_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile* out);
 
+/* The vendor-library ceiling row of the 16-bit GEMM (rocBLAS gemm_ex, fp32
+ * compute), the counterpart of MCKE_GEMM_CUBLAS_REF for these types: same
+ * arguments as mcke_launch_gemm_lp without the tile. */
+int mcke_launch_gemm_lp_vendor(const void* a, const void* b, void* c, int ab_dtype,
+                               int c_dtype, int64_t m, int64_t n, int64_t k, float alpha,
+                               float beta, void* stream);
+
 /* ---- runtime: rt::Stream / rt::Event / raw device memory ------------------
  * reference include/mcke/runtime/stream.hpp:82-306, src/core/device.cpp:56-168,
  * src/memory/allocator.cpp:44-73, src/tensor/tensor.cpp:108-138. */

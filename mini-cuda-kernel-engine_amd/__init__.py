@@ -190,6 +190,8 @@ def lib() -> C.CDLL:
         "mcke_gemm_lp_kernel_attrs": (C.c_int, [C.c_int, C.c_int, C.POINTER(GemmTile),
                                                 C.POINTER(KernelAttrs)]),
         "mcke_gemm_lp_default_tile": (C.c_int, [_I64, _I64, _I64, C.POINTER(GemmTile)]),
+        "mcke_launch_gemm_lp_vendor": (C.c_int, [_VP, _VP, _VP, C.c_int, C.c_int, _I64, _I64,
+                                                 _I64, C.c_float, C.c_float, _VP]),
         "mcke_rt_get_device_count": (C.c_int, [C.POINTER(C.c_int)]),
         "mcke_rt_set_device": (C.c_int, [C.c_int]),
         "mcke_rt_get_device": (C.c_int, [C.POINTER(C.c_int)]),
@@ -517,6 +519,13 @@ def launch_gemm_lp(a, b, c, ab_dtype, c_dtype, m: int, n: int, k: int, alpha: fl
     tile = gemm_lp_default_tile(m, n, k) if tile is None else tile
     return _st(lib().mcke_launch_gemm_lp(_ptr(a), _ptr(b), _ptr(c), int(ab_dtype), int(c_dtype),
                                          m, n, k, alpha, beta, C.byref(tile), _sh(stream)))
+
+
+def launch_gemm_lp_vendor(a, b, c, ab_dtype, c_dtype, m: int, n: int, k: int, alpha: float,
+                          beta: float, stream=None) -> Status:
+    """The vendor-library ceiling row of the 16-bit GEMM (rocBLAS gemm_ex)."""
+    return _st(lib().mcke_launch_gemm_lp_vendor(_ptr(a), _ptr(b), _ptr(c), int(ab_dtype),
+                                                int(c_dtype), m, n, k, alpha, beta, _sh(stream)))
 
 
 def gemm_lp_kernel_attrs(ab_dtype, c_dtype, tile: GemmTile):

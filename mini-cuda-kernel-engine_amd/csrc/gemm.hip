@@ -439,6 +439,34 @@ int mcke_gemm_kernel_attrs(int variant, const mcke_gemm_tile* tile, mcke_kernel_
   return ok();
 }
 
+int mcke_launch_gemm_lp_vendor(const void* a, const void* b, void* c, int ab_dtype,
+                               int c_dtype, int64_t m, int64_t n, int64_t k, float alpha,
+                               float beta, void* stream) {
+  if ((ab_dtype != MCKE_DTYPE_BF16 && ab_dtype != MCKE_DTYPE_F16) ||
+      (c_dtype != MCKE_DTYPE_F32 && c_dtype != ab_dtype))
+    return invalid("launch_gemm_lp_vendor: (ab_dtype, c_dtype) must be (BF16|F16, F32|ab_dtype)");
+  if (m == 0 || n == 0) return ok();
+  if (m < 0 || n < 0 || k < 0) return invalid("launch_gemm_lp_vendor: negative extent");
+  if (!a || !b || !c) return invalid("launch_gemm_lp_vendor: null pointer");
+  if (a == c || b == c) return invalid("launch_gemm_lp_vendor: output aliases an input");
+  if (m > 2147483647LL || n > 2147483647LL || k > 2147483647LL)
+    return invalid("launch_gemm_lp_vendor: extent exceeds INT32_MAX");
+  rocblas_handle h = nullptr;
+  if (int rc = rocblas_for_stream(static_cast<hipStream_t>(stream), &h)) return rc;
+  const rocblas_datatype ab =
+      ab_dtype == MCKE_DTYPE_BF16 ? rocblas_datatype_bf16_r : rocblas_datatype_f16_r;
+  const rocblas_datatype cd = c_dtype == MCKE_DTYPE_F32 ? rocblas_datatype_f32_r : ab;
+  const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
+  // Row-major C = A B is the column-major C^T = B^T A^T: operands swapped.
+  const rocblas_status st = rocblas_gemm_ex(
+      h, rocblas_operation_none, rocblas_operation_none, ni, mi, ki, &alpha, b, ab, ni, a, ab, ki,
+      &beta, c, cd, ni, c, cd, ni, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (st != rocblas_status_success)
+    return fail(MCKE_STATUS_DEVICE_ERROR,
+                std::string("rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
+  return ok();
+}
+
 int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile* out) {
   if (!out) return invalid("gemm_mfma_default_tile: null out");
   (void)k;

@@ -191,3 +191,19 @@ def test_kernel_attrs(gpu):
             assert at.local_bytes == 0, (tile, ab, cd)        # no spills on the whole-tile path
             assert at.static_smem_bytes == 2 * (tile.bm + tile.bn) * 128
             assert at.threads_per_block == 256 and at.max_blocks_per_sm_api >= 1
+
+
+@pytest.mark.parametrize("dt", DTS, ids=DT_ID.get)
+def test_vendor_ceiling_row_matches_oracle(gpu, orc, dt):
+    # The rocBLAS row the benchmark compares against computes the same product.
+    M, N, K = 192, 320, 256
+    a16 = orc.to_16(orc.fill_random(M * K, 21), dt)
+    b16 = orc.to_16(orc.fill_random(K * N, 22), dt)
+    D = gpu.DeviceBuffer
+    da, db, dc = D.from_array(a16), D.from_array(b16), D(M * N * 4)
+    st = gpu.launch_gemm_lp_vendor(da, db, dc, dt, F32, M, N, K, 1.0, 0.0)
+    assert st.ok(), str(st)
+    gpu.device_synchronize()
+    want = orc.gemm_lp(a16, b16, np.zeros(M * N, np.float32), M, N, K, 1.0, 0.0, dt, F32)
+    r = orc.compare(dc.download(M * N), want, orc.tol_gemm(K), orc.abs_tol_gemm(K))
+    assert r.ok, str(r)
