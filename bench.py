@@ -91,6 +91,7 @@ class Op:
         self.single_ms: list[float] = []
         self.verify = None       # callable(oracle) -> dict, run in the CPU leg
         self.parity = None
+        self.copy_peak = None    # measured 1R+1W ceiling (GB/s), when measured
 
     def summary(self, measured_peak=None, traffic=None):
         avg = self.total_ms / self.launches
@@ -117,6 +118,9 @@ class Op:
             out["hbm_traffic_bytes"] = traffic
         if self.parity is not None:
             out["parity"] = self.parity
+        if self.copy_peak and self.name.startswith(("softmax", "bias_gelu")):
+            out["measured_copy_peak"] = round(self.copy_peak, 1)
+            out["frac_of_copy"] = round(achieved / self.copy_peak, 4)
         return out
 
 
@@ -364,11 +368,25 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     got = arrs[1][2].download(16)
     if not np.all(got == 7.0):
         raise RuntimeError(f"stream triad produced {got[:4]}, expected 7.0")
+    # The read+write ceiling (one read, one write per element), for softmax and bias+act.
+    for s in range(2):
+        ck(m.launch_stream_copy_f32(arrs[s][0], arrs[s][2], nt, stream))
+    e0.record(stream)
+    for s in range(reps):
+        m.launch_stream_copy_f32(arrs[s % 2][0], arrs[s % 2][2], nt, stream)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    out["stream_copy_gb_s"] = round(2 * nt * 4 / (ms * 1e-3) / 1e9, 1)
+    if not np.all(arrs[1][2].download(16) == 1.0):
+        raise RuntimeError("stream copy produced wrong values")
     out["note"] = ("mfma: blocks = 2 x CUs, 4 waves each, 4 chains of v_mfma_f32_32x32x2_f32, "
                    f"{mfma_iters} iterations (~GEMM launch length); triad: a = 3c + b over "
-                   "3 x 256 MiB, two rotating sets")
+                   "3 x 256 MiB, two rotating sets; copy: y = x over 2 x 256 MiB, one float4 "
+                   "per lane, non-temporal, two rotating sets (the 1-read + 1-write ceiling "
+                   "of softmax and bias+act, frac_of_copy)")
     log(f"measured peaks: MFMA fp32 {out['mfma_f32_tflops']} TFLOP/s, "
-        f"triad {out['stream_triad_gb_s']} GB/s")
+        f"triad {out['stream_triad_gb_s']} GB/s, copy {out['stream_copy_gb_s']} GB/s")
     return out
 
 
@@ -738,6 +756,7 @@ def main(argv=None) -> int:
     traffic = profiled_traffic()
     summaries = []
     for op in ops:
+        op.copy_peak = peaks["stream_copy_gb_s"] if peaks else None
         mp = None
         if peaks:
             mp = peaks["mfma_f32_tflops"] if op.bound == "mfma" else peaks["stream_triad_gb_s"]

@@ -268,6 +268,10 @@ int mcke_launch_mfma_peak_f32(const float* seed, float* out, int64_t blocks, int
                               void* stream);
 int mcke_launch_stream_triad_f32(const float* b, const float* c, float* a, float scalar, int64_t n,
                                  void* stream);
+/* stream_copy: y[i] = x[i] for i < n (8 bytes per element), the read+write
+ * ceiling (no reference counterpart; the reference's bench measures the triad
+ * only); 16-byte aligned x, y; y must not alias x. */
+int mcke_launch_stream_copy_f32(const float* x, float* y, int64_t n, void* stream);
 /* The 16-bit MFMA counterpart of mfma_peak (no reference counterpart: the
  * ceiling of mcke_launch_gemm_lp): the same 4 chains per wave of
  * v_mfma_f32_32x32x16_{bf16,f16} (ab_dtype MCKE_DTYPE_BF16 or MCKE_DTYPE_F16),

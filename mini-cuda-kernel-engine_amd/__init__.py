@@ -216,6 +216,7 @@ def lib() -> C.CDLL:
         "mcke_rt_memset_async": (C.c_int, [_VP, C.c_int, C.c_size_t, _VP]),
         "mcke_mfma_peak_flops": (C.c_uint64, [_I64, _I64]),
         "mcke_launch_mfma_peak_f32": (C.c_int, [_VP, _VP, _I64, _I64, _VP]),
+        "mcke_launch_stream_copy_f32": (C.c_int, [_VP, _VP, _I64, _VP]),
         "mcke_mfma_peak_lp_flops": (C.c_uint64, [_I64, _I64]),
         "mcke_launch_mfma_peak_lp": (C.c_int, [C.c_int, _VP, _VP, _I64, _I64, _VP]),
         "mcke_launch_stream_triad_f32": (C.c_int, [_VP, _VP, _VP, C.c_float, _I64, _VP]),
@@ -551,6 +552,10 @@ def mfma_peak_flops(blocks: int, iters: int) -> int:
 
 def launch_mfma_peak_f32(seed, out, blocks: int, iters: int, stream=None) -> Status:
     return _st(lib().mcke_launch_mfma_peak_f32(_ptr(seed), _ptr(out), blocks, iters, _sh(stream)))
+
+
+def launch_stream_copy_f32(x, y, n: int, stream=None) -> Status:
+    return _st(lib().mcke_launch_stream_copy_f32(_ptr(x), _ptr(y), n, _sh(stream)))
 
 
 def mfma_peak_lp_flops(blocks: int, iters: int) -> int:

@@ -110,6 +110,25 @@ __global__ __launch_bounds__(kTriadThreads) void stream_triad_kernel(const float
   if (t < n) a[t] = fmaf(s, c[t], b[t]);
 }
 
+// The read+write ceiling for kernels that move one read and one write per
+// element (softmax, bias+act): y = x, one float4 per lane, non-temporal both
+// ways, one launch covering the array with no grid-stride loop.  Of the copy
+// shapes measured on MI355X (grid-stride loops at 256..16384 workgroups, 1..8
+// float4 per lane, plain or non-temporal accesses), this one moves the most.
+constexpr int kCopyThreads = 256;
+
+__global__ __launch_bounds__(kCopyThreads) void stream_copy_kernel(const float* __restrict__ x,
+                                                                   float* __restrict__ y,
+                                                                   int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kCopyThreads + threadIdx.x;
+  const int64_t n4 = n / 4;
+  if (i < n4) {
+    st_stream(reinterpret_cast<f32x4*>(y) + i, ld_stream(reinterpret_cast<const f32x4*>(x) + i));
+  } else if (i == n4) {
+    for (int64_t t = 4 * n4; t < n; ++t) y[t] = x[t];
+  }
+}
+
 }  // namespace
 }  // namespace mcke_amd
 
@@ -174,6 +193,23 @@ int mcke_launch_stream_triad_f32(const float* b, const float* c, float* a, float
   stream_triad_kernel<<<static_cast<unsigned>(blocks), kTriadThreads, 0,
                         static_cast<hipStream_t>(stream)>>>(b, c, a, scalar, n);
   MCKE_LAUNCH_CHECK("stream_triad_kernel");
+  return ok();
+}
+
+int mcke_launch_stream_copy_f32(const float* x, float* y, int64_t n, void* stream) {
+  if (n == 0) return ok();
+  if (n < 0) return invalid("launch_stream_copy_f32: negative n");
+  if (!x || !y) return invalid("launch_stream_copy_f32: null pointer");
+  if (!aligned(x, 16) || !aligned(y, 16))
+    return invalid("launch_stream_copy_f32: pointers must be 16-byte aligned");
+  if (x == y) return invalid("launch_stream_copy_f32: output aliases the input");
+  // One lane per float4 plus one lane for the tail (n % 4 elements).
+  const int64_t lanes = n / 4 + 1;
+  const int64_t blocks = (lanes + kCopyThreads - 1) / kCopyThreads;
+  if (blocks > 0x7fffffff) return invalid("launch_stream_copy_f32: n too large for one launch");
+  stream_copy_kernel<<<static_cast<unsigned>(blocks), kCopyThreads, 0,
+                       static_cast<hipStream_t>(stream)>>>(x, y, n);
+  MCKE_LAUNCH_CHECK("stream_copy_kernel");
   return ok();
 }
 

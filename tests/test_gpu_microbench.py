@@ -1,6 +1,7 @@
 """GPU tests of the measured-denominator kernels (mcke_launch_mfma_peak_f32,
 mcke_launch_stream_triad_f32), the counterparts of the reference's
-bench/fma_peak.cu and bench/stream_triad.cu.
+bench/fma_peak.cu and bench/stream_triad.cu, and of the 16-bit MFMA chains and the
+read+write copy ceiling this build adds.
 
 Both are checked for exact results, so a rate measured with them is a rate of
 work that was really done: the triad on quarter-multiple inputs (every fma is
@@ -81,3 +82,57 @@ def test_stream_triad_rejects_alias_and_misalignment(mcke, gpu):
     assert m.launch_stream_triad_f32(d.ptr + 4, e, e.ptr + 2048, 1.0, 64).code == \
         m.StatusCode.kInvalidArgument
     assert m.launch_stream_triad_f32(d, e, e, 1.0, 0).ok()
+
+
+def _mfma_peak_lp_expected(seed: np.ndarray, blocks: int, iters: int) -> np.ndarray:
+    """out[block*256 + t] for the 16-bit chains: thread t (wave w = t/64, lane
+    l = t%64) feeds A values seed[(t + e) % 256] and B values seed[(t + 8 + e) % 256],
+    e = 0..7.  Whatever k each (lane half h, element e) slot stands for, A and B
+    share it, so C[i][j] = sum over h, e of A(lane i + 32h, e) * B(lane j + 32h, e);
+    the accumulator layout is the 32x32 one of the fp32 chains."""
+    out = np.zeros(256, dtype=np.float64)
+    for w in range(4):
+        c = np.zeros((32, 32))
+        for i in range(32):
+            for j in range(32):
+                acc = 0.0
+                for h in range(2):
+                    ta, tb = 64 * w + i + 32 * h, 64 * w + j + 32 * h
+                    for e in range(8):
+                        acc += seed[(ta + e) % 256] * seed[(tb + 8 + e) % 256]
+                c[i, j] = acc
+        c *= iters
+        for l in range(64):
+            s = 0.0
+            for r in range(16):
+                s += c[8 * (r // 4) + 4 * (l // 32) + r % 4, l % 32]
+            out[64 * w + l] = 4 * s
+    return np.tile(out, blocks).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", [2, 1], ids=["bf16", "f16"])
+def test_mfma_peak_lp_closed_form(mcke, gpu, dt):
+    m = mcke
+    seed = (np.arange(256) % 7 - 3).astype(np.float32)     # exact in bf16 and fp16
+    blocks, iters = 4, 500
+    d_seed = m.DeviceBuffer.from_array(seed)
+    out = m.DeviceBuffer(blocks * 256 * 4)
+    m.launch_mfma_peak_lp(dt, d_seed, out, blocks, iters).throw_if_error()
+    m.device_synchronize()
+    assert np.array_equal(out.download(blocks * 256), _mfma_peak_lp_expected(seed, blocks, iters))
+    assert m.mfma_peak_lp_flops(blocks, iters) == blocks * 4 * iters * 4 * 32768
+    assert m.launch_mfma_peak_lp(0, d_seed, out, blocks, iters).code == \
+        m.StatusCode.kInvalidArgument
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 7, 1000, 4097, 1 << 20])
+def test_stream_copy_exact(mcke, gpu, n):
+    m = mcke
+    x = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    dx = m.DeviceBuffer.from_array(x)
+    dy = m.DeviceBuffer(max(4, n) * 4)
+    m.launch_stream_copy_f32(dx, dy, n).throw_if_error()
+    m.device_synchronize()
+    assert np.array_equal(dy.download(n), x)
+    assert m.launch_stream_copy_f32(dx, dx, n).code == m.StatusCode.kInvalidArgument
+    assert m.launch_stream_copy_f32(dx.ptr + 4, dy, 8).code == m.StatusCode.kInvalidArgument
