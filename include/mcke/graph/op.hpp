@@ -53,6 +53,10 @@ class Op {
       const std::vector<Shape>& input_shapes) const = 0;
   [[nodiscard]] virtual OpCost cost(const std::vector<Shape>& input_shapes) const = 0;
   [[nodiscard]] virtual std::size_t workspace_bytes(const std::vector<Shape>&) const { return 0; }
+  // Element type of the outputs from those of the inputs (no reference
+  // counterpart: the reference's graph is fp32 throughout).  The default accepts
+  // fp32 inputs only and produces fp32; GemmOp also takes 16-bit inputs.
+  [[nodiscard]] virtual StatusOr<DType> infer_dtype(const std::vector<DType>& input_dtypes) const;
 };
 
 using OpPtr = std::unique_ptr<Op>;
@@ -63,7 +67,13 @@ struct GemmParams {
   using Variant = kernels::GemmVariant;
   Variant variant = Variant::kTiledRegBlock;
   kernels::GemmTile tile{};
-  bool auto_tile = false;   // kMfmaF32 only: pick the tile per shape at launch
+  bool auto_tile = false;   // kMfmaF32 (or 16-bit inputs): pick the tile per shape at launch
+  // Element types (this build's addition).  kF32 inputs run `variant`;
+  // kBF16 / kF16 inputs run the 16-bit MFMA GEMM (kernels::launch_gemm_lp, whose
+  // tiles are gemm_lp_tile_is_supported's), with C in out_dtype (kF32 or the
+  // input type).
+  DType in_dtype = DType::kF32;
+  DType out_dtype = DType::kF32;
 };
 
 class GemmOp final : public Op {
@@ -74,6 +84,7 @@ class GemmOp final : public Op {
                               const std::vector<Tensor>&) override;
   [[nodiscard]] StatusOr<std::vector<Shape>> infer_shapes(const std::vector<Shape>&) const override;
   [[nodiscard]] OpCost cost(const std::vector<Shape>&) const override;
+  [[nodiscard]] StatusOr<DType> infer_dtype(const std::vector<DType>&) const override;
   [[nodiscard]] const GemmParams& params() const noexcept { return p_; }
 
  private:

@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <string>
 
+#include "mcke/core/dtype.hpp"
 #include "mcke/core/status.hpp"
 #include "mcke/kernels/gemm_tile.hpp"
 #include "mcke/runtime/stream.hpp"
@@ -130,6 +131,36 @@ struct GemmKernelAttrs {
   mcke_gemm_tile t{};
   (void)mcke_gemm_mfma_default_tile(m, n, k, &t);
   return GemmTile{t.bm, t.bn, t.bk, t.tm, t.tn};
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit-input GEMM.  No reference counterpart: the reference reserves
+// DType::kF16 / kBF16 (dtype.hpp:33-41) but launches fp32 only.  A and B hold
+// `ab` values (kBF16 or kF16), products accumulate in fp32, C holds `c` values
+// (kF32 or `ab`).  Argument order, validation and status codes follow
+// launch_gemm_f32.
+// ---------------------------------------------------------------------------
+[[nodiscard]] inline Status launch_gemm_lp(const void* a, const void* b, void* c, DType ab, DType cd,
+                                          std::int64_t m, std::int64_t n, std::int64_t k,
+                                          float alpha, float beta, GemmTile tile,
+                                          rt::StreamHandle stream) {
+  const mcke_gemm_tile t = detail::to_c(tile);
+  return detail::status_of(mcke_launch_gemm_lp(a, b, c, static_cast<int>(ab), static_cast<int>(cd),
+                                               m, n, k, alpha, beta, &t, stream));
+}
+
+// The 16-bit GEMM tile this build picks for a shape.
+[[nodiscard]] inline GemmTile lp_default_tile(std::int64_t m, std::int64_t n, std::int64_t k) {
+  mcke_gemm_tile t{};
+  (void)mcke_gemm_lp_default_tile(m, n, k, &t);
+  return GemmTile{t.bm, t.bn, t.bk, t.tm, t.tn};
+}
+
+// Whether the 16-bit GEMM is instantiated for a tile: (256,256,64,16,16),
+// (128,128,64,8,8) or (64,64,64,4,4).
+[[nodiscard]] constexpr bool gemm_lp_tile_is_supported(const GemmTile& t) {
+  return t.bk == 64 && t.bm == t.bn && (t.bm == 256 || t.bm == 128 || t.bm == 64) &&
+         t.tm == t.bm / 16 && t.tn == t.bn / 16;
 }
 
 }  // namespace mcke::kernels

@@ -89,6 +89,18 @@ mcke_graph* mcke_graph_create(void);
 void mcke_graph_destroy(mcke_graph* g);
 int mcke_graph_add_input(mcke_graph* g, const int64_t* dims, int rank, const char* name, uint32_t* out_tensor);
 /* GemmOp with beta = 0; tile == NULL means "pick per shape" (kMfmaF32 only). */
+/* An input tensor of element type `dtype` (MCKE_DTYPE_F32, _F16 or _BF16; the
+ * reference's graph is fp32 only, and mcke_graph_add_input makes fp32 inputs). */
+int mcke_graph_add_input_typed(mcke_graph* g, const int64_t* dims, int rank, int dtype,
+                               const char* name, uint32_t* out_tensor);
+
+/* A GEMM node on 16-bit inputs (a and b bf16, or both f16): C = alpha * A B in
+ * out_dtype (MCKE_DTYPE_F32 or the input type), through mcke_launch_gemm_lp.
+ * NULL tile = the per-shape default.  The other operators take f32 tensors only;
+ * a node given 16-bit inputs fails at build time. */
+int mcke_graph_add_gemm_lp(mcke_graph* g, uint32_t a, uint32_t b, float alpha, int out_dtype,
+                           const mcke_gemm_tile* tile, const char* name, uint32_t* out_tensor);
+
 int mcke_graph_add_gemm(mcke_graph* g, uint32_t a, uint32_t b, float alpha, int variant,
                         const mcke_gemm_tile* tile, const char* name, uint32_t* out_tensor);
 int mcke_graph_add_bias_act(mcke_graph* g, uint32_t x, uint32_t bias, int act, int vector_width,

@@ -90,6 +90,10 @@ def host_lib() -> C.CDLL:
         "mcke_graph_create": (_VP, []),
         "mcke_graph_destroy": (None, [_VP]),
         "mcke_graph_add_input": (C.c_int, [_VP, C.POINTER(C.c_int64), C.c_int, C.c_char_p, _U32P]),
+        "mcke_graph_add_input_typed": (C.c_int, [_VP, C.POINTER(C.c_int64), C.c_int, C.c_int,
+                                                 C.c_char_p, _U32P]),
+        "mcke_graph_add_gemm_lp": (C.c_int, [_VP, _U32, _U32, C.c_float, C.c_int,
+                                             C.POINTER(GemmTile), C.c_char_p, _U32P]),
         "mcke_graph_add_gemm": (C.c_int, [_VP, _U32, _U32, C.c_float, C.c_int, C.POINTER(GemmTile),
                                           C.c_char_p, _U32P]),
         "mcke_graph_add_bias_act": (C.c_int, [_VP, _U32, _U32, C.c_int, C.c_int, C.c_char_p, _U32P]),
@@ -138,7 +142,8 @@ def _check(rc: int) -> None:
 
 
 class Graph:
-    """A DAG of kernel-backed ops over f32 tensors (reference Graph)."""
+    """A DAG of kernel-backed ops (reference Graph).  Tensors are f32 unless an
+    input is declared bf16 / f16 (`dtype`); only GEMM nodes take 16-bit inputs."""
 
     def __init__(self):
         self.h = host_lib().mcke_graph_create()
@@ -148,13 +153,28 @@ class Graph:
         _check(rc)
         return int(out.value)
 
-    def add_input(self, shape, name: str) -> int:
+    def add_input(self, shape, name: str, dtype: int = 0) -> int:
+        """dtype: 0 f32 (the default), 1 f16, 2 bf16 (DType numbering)."""
         dims = (C.c_int64 * len(shape))(*shape)
         out = C.c_uint32()
-        t = self._out(host_lib().mcke_graph_add_input(self.h, dims, len(shape), name.encode(),
-                                                      C.byref(out)), out)
+        if int(dtype) == 0:
+            rc = host_lib().mcke_graph_add_input(self.h, dims, len(shape), name.encode(),
+                                                 C.byref(out))
+        else:
+            rc = host_lib().mcke_graph_add_input_typed(self.h, dims, len(shape), int(dtype),
+                                                       name.encode(), C.byref(out))
+        t = self._out(rc, out)
         self.names[t] = name
         return t
+
+    def add_gemm_lp(self, a: int, b: int, name: str, out_dtype: int = 0,
+                    tile: GemmTile | None = None, alpha: float = 1.0) -> int:
+        """GEMM on 16-bit inputs (a, b both bf16 or both f16); C in out_dtype
+        (0 = f32, or the input type).  tile None: the per-shape default."""
+        out = C.c_uint32()
+        tp = C.byref(tile) if tile is not None else None
+        return self._out(host_lib().mcke_graph_add_gemm_lp(self.h, a, b, alpha, int(out_dtype), tp,
+                                                           name.encode(), C.byref(out)), out)
 
     def add_gemm(self, a: int, b: int, name: str, variant=GemmVariant.kMfmaF32,
                  tile: GemmTile | None = None, alpha: float = 1.0) -> int:
@@ -218,7 +238,8 @@ class Executor:
         _check(host_lib().mcke_executor_plan(self.h))
 
     def set_input(self, t: int, arr: np.ndarray) -> None:
-        arr = np.ascontiguousarray(arr, dtype=np.float32)
+        """f32 tensors take float arrays; 16-bit tensors take uint16 bit patterns."""
+        arr = np.ascontiguousarray(arr, dtype=np.uint16 if arr.dtype == np.uint16 else np.float32)
         _check(host_lib().mcke_executor_set_input(self.h, t, arr.ctypes.data, arr.nbytes))
 
     def run_async(self) -> None:
@@ -241,8 +262,9 @@ class Executor:
         _check(host_lib().mcke_executor_is_captured(self.h, C.byref(out)))
         return bool(out.value)
 
-    def read(self, t: int, numel: int) -> np.ndarray:
-        out = np.empty(numel, dtype=np.float32)
+    def read(self, t: int, numel: int, dtype=np.float32) -> np.ndarray:
+        """dtype np.uint16 reads a 16-bit tensor's bit patterns."""
+        out = np.empty(numel, dtype=dtype)
         _check(host_lib().mcke_executor_read_tensor(self.h, t, out.ctypes.data, out.nbytes))
         return out
 

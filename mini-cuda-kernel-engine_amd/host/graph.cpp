@@ -68,13 +68,19 @@ StatusOr<std::vector<TensorId>> Graph::add_node(OpPtr op, std::vector<TensorId> 
   }
   MCKE_ASSIGN_OR_RETURN(std::vector<Shape> outs, op->infer_shapes(shapes));
   if (outs.empty()) return InvalidArgumentError(where + ": the op produced no outputs");
+  std::vector<DType> dtypes;
+  dtypes.reserve(inputs.size());
+  for (TensorId t : inputs) dtypes.push_back(tensors_[t].dtype);
+  auto out_dtype = op->infer_dtype(dtypes);
+  if (!out_dtype.ok())
+    return Status(out_dtype.status().code(), where + ": " + out_dtype.status().message());
   const auto nid = static_cast<NodeId>(nodes_.size());
   std::vector<TensorId> out_ids;
   for (std::size_t k = 0; k < outs.size(); ++k) {
     MCKE_RETURN_IF_ERROR(check_shape(outs[k], where + " output " + std::to_string(k)));
     TensorDesc d;
     d.shape = outs[k];
-    d.dtype = inputs.empty() ? DType::kF32 : tensors_[inputs[0]].dtype;
+    d.dtype = *out_dtype;
     d.producer = nid;
     d.name = outs.size() > 1 ? name + ":" + std::to_string(k) : name;
     tensors_.push_back(std::move(d));

@@ -62,6 +62,34 @@ int mcke_graph_add_input(mcke_graph* g, const int64_t* dims, int rank, const cha
   return MCKE_STATUS_OK;
 }
 
+int mcke_graph_add_input_typed(mcke_graph* g, const int64_t* dims, int rank, int dtype,
+                               const char* name, uint32_t* out) {
+  if (!g || !dims || !out) return bad("mcke_graph_add_input_typed: null argument");
+  if (rank < 1 || rank > mcke::kMaxRank) return bad("mcke_graph_add_input_typed: rank must be 1..5");
+  if (dtype != MCKE_DTYPE_F32 && dtype != MCKE_DTYPE_F16 && dtype != MCKE_DTYPE_BF16)
+    return bad("mcke_graph_add_input_typed: dtype must be MCKE_DTYPE_F32, _F16 or _BF16");
+  auto r = g->g.add_input(mcke::Shape(dims, rank), static_cast<mcke::DType>(dtype), name ? name : "");
+  if (!r.ok()) return code(r.status());
+  *out = *r;
+  return MCKE_STATUS_OK;
+}
+
+int mcke_graph_add_gemm_lp(mcke_graph* g, uint32_t a, uint32_t b, float alpha, int out_dtype,
+                           const mcke_gemm_tile* tile, const char* name, uint32_t* out) {
+  if (!g || !out) return bad("mcke_graph_add_gemm_lp: null argument");
+  if (a >= g->g.num_tensors()) return bad("mcke_graph_add_gemm_lp: tensor a is out of range");
+  mcke::GemmParams p;
+  p.alpha = alpha;
+  p.beta = 0.0f;
+  p.in_dtype = g->g.tensor(a).dtype;
+  p.out_dtype = static_cast<mcke::DType>(out_dtype);
+  if (p.in_dtype != mcke::DType::kBF16 && p.in_dtype != mcke::DType::kF16)
+    return bad("mcke_graph_add_gemm_lp: tensor a must be bf16 or f16");
+  if (tile) p.tile = mcke::kernels::GemmTile{tile->bm, tile->bn, tile->bk, tile->tm, tile->tn};
+  else p.auto_tile = true;
+  return add_op<mcke::GemmOp>(g, std::make_unique<mcke::GemmOp>(p), {a, b}, name, out);
+}
+
 int mcke_graph_add_gemm(mcke_graph* g, uint32_t a, uint32_t b, float alpha, int variant,
                         const mcke_gemm_tile* tile, const char* name, uint32_t* out) {
   mcke::GemmParams p;

@@ -47,9 +47,39 @@ std::string tile_str(const kernels::GemmTile& t) {
          std::to_string(t.tm) + "," + std::to_string(t.tn) + ")";
 }
 
+bool lp_dtype(DType t) { return t == DType::kBF16 || t == DType::kF16; }
+
 }  // namespace
 
+StatusOr<DType> Op::infer_dtype(const std::vector<DType>& in) const {
+  for (std::size_t i = 0; i < in.size(); ++i)
+    if (in[i] != DType::kF32)
+      return InvalidArgumentError(std::string(type_name()) + ": input " + std::to_string(i) +
+                                  " is " + std::string(dtype_name(in[i])) +
+                                  "; this operator runs on f32 tensors only");
+  return DType::kF32;
+}
+
 // ---------------------------------------------------------------------------
+StatusOr<DType> GemmOp::infer_dtype(const std::vector<DType>& in) const {
+  if (in.size() != 2)
+    return InvalidArgumentError("GemmOp: expects 2 inputs (A, B), got " + std::to_string(in.size()));
+  if (in[0] != p_.in_dtype || in[1] != p_.in_dtype)
+    return InvalidArgumentError("GemmOp: inputs are " + std::string(dtype_name(in[0])) + " and " +
+                                std::string(dtype_name(in[1])) + " but the op was built for " +
+                                std::string(dtype_name(p_.in_dtype)));
+  if (p_.in_dtype == DType::kF32) {
+    if (p_.out_dtype != DType::kF32)
+      return InvalidArgumentError("GemmOp: f32 inputs produce f32 C");
+    return DType::kF32;
+  }
+  if (!lp_dtype(p_.in_dtype))
+    return InvalidArgumentError("GemmOp: inputs must be f32, bf16 or f16");
+  if (p_.out_dtype != DType::kF32 && p_.out_dtype != p_.in_dtype)
+    return InvalidArgumentError("GemmOp: 16-bit inputs produce C in f32 or the input type");
+  return p_.out_dtype;
+}
+
 StatusOr<std::vector<Shape>> GemmOp::infer_shapes(const std::vector<Shape>& in) const {
   if (in.size() != 2)
     return InvalidArgumentError("GemmOp: expects 2 inputs (A, B), got " + std::to_string(in.size()));
@@ -64,6 +94,13 @@ StatusOr<std::vector<Shape>> GemmOp::infer_shapes(const std::vector<Shape>& in) 
   if (p_.beta != 0.0f)
     return UnimplementedError("GemmOp: beta != 0 reads C, which the graph does not model as an "
                               "input; add the term with a separate node");
+  if (lp_dtype(p_.in_dtype)) {
+    if (!p_.auto_tile && !kernels::gemm_lp_tile_is_supported(p_.tile))
+      return InvalidArgumentError("GemmOp: tile " + tile_str(p_.tile) +
+                                  " is not instantiated for the 16-bit GEMM ((256,256,64,16,16), "
+                                  "(128,128,64,8,8), (64,64,64,4,4))");
+    return std::vector<Shape>{Shape{m, n}};
+  }
   const bool auto_mfma = p_.auto_tile && p_.variant == kernels::GemmVariant::kMfmaF32;
   if (!auto_mfma && !kernels::gemm_tile_is_supported(p_.variant, p_.tile))
     return InvalidArgumentError("GemmOp: tile " + tile_str(p_.tile) +
@@ -80,7 +117,7 @@ OpCost GemmOp::cost(const std::vector<Shape>& in) const {
   const auto k = static_cast<std::uint64_t>(in[0].dim(1));
   const auto n = static_cast<std::uint64_t>(in[1].dim(1));
   c.flops = 2ull * m * n * k;
-  c.bytes = (m * k + k * n + m * n) * sizeof(float);
+  c.bytes = (m * k + k * n) * dtype_size(p_.in_dtype) + m * n * dtype_size(p_.out_dtype);
   return c;
 }
 
@@ -88,6 +125,17 @@ Status GemmOp::launch(const OpContext& ctx, const std::vector<Tensor>& inputs,
                       const std::vector<Tensor>& outputs) {
   if (inputs.size() != 2 || outputs.size() != 1)
     return InvalidArgumentError("GemmOp::launch: expects 2 inputs and 1 output");
+  if (lp_dtype(p_.in_dtype)) {
+    if (inputs[0].dtype() != p_.in_dtype || inputs[1].dtype() != p_.in_dtype ||
+        outputs[0].dtype() != p_.out_dtype)
+      return InvalidArgumentError("GemmOp::launch: tensor types do not match the op's");
+    const dim_t m = inputs[0].shape().dim(0), k = inputs[0].shape().dim(1),
+                n = inputs[1].shape().dim(1);
+    const kernels::GemmTile tile = p_.auto_tile ? kernels::lp_default_tile(m, n, k) : p_.tile;
+    return kernels::launch_gemm_lp(inputs[0].data_ptr(), inputs[1].data_ptr(), outputs[0].data_ptr(),
+                                   p_.in_dtype, p_.out_dtype, m, n, k, p_.alpha, p_.beta, tile,
+                                   ctx.stream);
+  }
   const float* a = inputs[0].data_as<float>();
   const float* b = inputs[1].data_as<float>();
   float* c = outputs[0].data_as<float>();

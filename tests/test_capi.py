@@ -74,6 +74,32 @@ def test_graph_builder_without_gpu(mcke):
         g2.add_gemm(x, x, "tiled_no_tile", variant=mcke.GemmVariant.kTiledSmem)
 
 
+def test_graph_dtypes_without_gpu(mcke):
+    """16-bit inputs: only GEMM nodes take them; the output dtype follows the op."""
+    from mcke_amd import graph
+    import pytest as _pt
+    IA = mcke.StatusCode.kInvalidArgument
+    g = graph.Graph()
+    x = g.add_input((64, 32), "x", dtype=2)          # bf16
+    w = g.add_input((32, 48), "w", dtype=2)
+    wh = g.add_input((32, 48), "wh", dtype=1)        # f16
+    b = g.add_input((48,), "b")                      # f32
+    h = g.add_gemm_lp(x, w, "g")                     # f32 C
+    assert g.shape(h) == (64, 48)
+    g.add_bias_act(h, b, "act")                      # f32 from here on
+    h16 = g.add_gemm_lp(x, w, "g16", out_dtype=2)    # bf16 C
+    for bad in (lambda: g.add_bias_act(h16, b, "act16"),          # f32-only op on bf16
+                lambda: g.add_softmax(x, "sm"),
+                lambda: g.add_gemm_lp(x, wh, "mixed"),             # bf16 x f16
+                lambda: g.add_gemm_lp(x, w, "odd_out", out_dtype=1),
+                lambda: g.add_gemm(x, w, "f32_variant_on_bf16"),
+                lambda: g.add_gemm_lp(b, b, "f32_inputs"),
+                lambda: g.add_gemm_lp(x, w, "tile", tile=mcke.GemmTile(256, 256, 32, 16, 16))):
+        with _pt.raises(mcke.MckeError) as ei:
+            bad()
+        assert ei.value.status.code == IA, ei.value
+
+
 def test_enum_values_match_reference(mcke):
     assert [int(v) for v in mcke.Activation] == [0, 1, 2, 3]
     assert [int(v) for v in mcke.ReduceKind] == [0, 1, 2]

@@ -279,3 +279,41 @@ def test_capture_refused_with_timing_probes(G):
         ex.capture()
     assert not ex.captured
     ex.close()
+
+
+@pytest.mark.parametrize("dt", [2, 1], ids=["bf16", "f16"])
+def test_16bit_gemm_node_feeds_f32_ops(G, orc, dt):
+    """A GEMM node on 16-bit inputs (the 16-bit MFMA kernel) with f32 C feeding
+    bias+GELU, and a second node writing 16-bit C, against the oracle on the
+    decoded inputs."""
+    T, D, F = 256, 128, 512
+    g = G.Graph()
+    x = g.add_input((T, D), "x", dtype=dt)
+    w1 = g.add_input((D, F), "W1", dtype=dt)
+    b1 = g.add_input((F,), "b1")
+    h32 = g.add_gemm_lp(x, w1, "gemm_lp")
+    h = g.add_bias_act(h32, b1, "bias_gelu", act=3)
+    h16 = g.add_gemm_lp(x, w1, "gemm_lp16", out_dtype=dt)
+    for t in (h32, h, h16):
+        g.mark_output(t)
+    ex = G.Executor(g, schedule=G.SchedulePolicy.kSequential,
+                    memory=G.MemoryPolicy.kAllocPerTensor, num_streams=1)
+    ex.plan()
+    xq = orc.to_16(orc.fill_normal(T * D, 11, 0.0, 1.0), dt)
+    wq = orc.to_16(orc.fill_normal(D * F, 12, 0.0, 0.02), dt)
+    bias = orc.fill_normal(F, 13, 0.0, 0.01)
+    ex.set_input(x, xq)
+    ex.set_input(w1, wq)
+    ex.set_input(b1, bias)
+    ex.run_sync()
+    got32 = ex.read(h32, T * F)
+    want32 = orc.gemm_lp(xq, wq, np.zeros(T * F, np.float32), T, F, D, 1.0, 0.0, dt, 0)
+    r = orc.compare(got32, want32, orc.tol_gemm(D), orc.abs_tol_gemm(D, 4.0 * 0.02 * 4.0))
+    assert r.ok, f"gemm_lp: {r}"
+    r = orc.compare(ex.read(h, T * F), orc.bias_act(got32, bias, T, F, 3), 1e-6, 1e-6)
+    assert r.ok, f"bias_gelu: {r}"
+    got16 = orc.from_16(ex.read(h16, T * F, np.uint16), dt)
+    want16 = orc.from_16(orc.to_16(want32, dt), dt)
+    ulp = 2.0 ** -7 if dt == 2 else 2.0 ** -10
+    r = orc.compare(got16, want16, orc.tol_gemm(D) + ulp, orc.abs_tol_gemm(D, 4.0 * 0.02 * 4.0))
+    assert r.ok, f"gemm_lp 16-bit C: {r}"
