@@ -469,16 +469,17 @@ int mcke_launch_gemm_lp_vendor(const void* a, const void* b, void* c, int ab_dty
 
 int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile* out) {
   if (!out) return invalid("gemm_mfma_default_tile: null out");
-  (void)k;
-  // Largest tile that still gives every CU of a 256-CU part four tiles (one
-  // workgroup per CU at a time, so four rounds): measured on MI355X, 256 x 256
-  // wins at 8192^3 (1024 tiles), 128 x 128 at 4096^3 and 64 x 64 at 2048^3,
-  // each over the next larger tile with a single round.  Smaller problems take
-  // the smallest tile.
-  const int64_t want = 4 * 256;
+  // One workgroup runs per CU at a time.  Measured on MI355X:
+  //   - 256 x 256 wins when every CU of a 256-CU part gets a tile and each CU's
+  //     share of K (rounds of tiles x K) is long enough to amortise a tile's
+  //     pipeline fill and epilogue: 8192^3 (4 rounds x 8192) and 4096 x 4096 x
+  //     16384 (1 round x 16384, 142 vs 136 TFLOP/s for 128 x 128);
+  //   - otherwise 128 x 128 wins with four rounds of tiles (4096^3: 130 vs 127),
+  //   - and 64 x 64 below that (2048^3).
   auto tiles = [&](int64_t t) { return ((m + t - 1) / t) * ((n + t - 1) / t); };
-  if (tiles(256) >= want) *out = mcke_gemm_tile{256, 256, 32, 16, 16};
-  else if (tiles(128) >= want) *out = mcke_gemm_tile{128, 128, 32, 8, 8};
+  const int64_t t256 = tiles(256);
+  if (t256 >= 256 && (t256 / 256) * k >= 16384) *out = mcke_gemm_tile{256, 256, 32, 16, 16};
+  else if (tiles(128) >= 4 * 256) *out = mcke_gemm_tile{128, 128, 32, 8, 8};
   else *out = mcke_gemm_tile{64, 64, 32, 4, 4};
   return ok();
 }

@@ -147,6 +147,9 @@ def test_default_mfma_tile(mcke):
     assert mcke.gemm_mfma_default_tile(4096, 4096, 4096).astuple() == (128, 128, 32, 8, 8)
     assert mcke.gemm_mfma_default_tile(2048, 2048, 2048).astuple() == (64, 64, 32, 4, 4)
     assert mcke.gemm_mfma_default_tile(512, 512, 512).astuple() == (64, 64, 32, 4, 4)
+    # Long K: one round of 256-tiles with K = 16384 (the MLP block's second GEMM).
+    assert mcke.gemm_mfma_default_tile(4096, 4096, 16384).astuple() == (256, 256, 32, 16, 16)
+    assert mcke.gemm_mfma_default_tile(8192, 8192, 2048).astuple() == (128, 128, 32, 8, 8)
 
 
 # ---------------------------------------------------------------------------
