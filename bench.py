@@ -657,6 +657,36 @@ def graph_section(m, steps=5, warmup=2):
         log(f"MLP {T2}x{D2}x{F2}: eager {cap['eager']['us_per_run']} us, "
             f"hipGraph {cap['hip_graph']['us_per_run']} us per run, same bits: {same}")
         out["mlp_small_capture"].append(entry)
+
+    # A launch-bound plan, on 4 streams and on one: eager (the host issues the
+    # launches, events and waits each run) vs one captured graph per run (on 4
+    # streams assembled node by node from single-stream captures).
+    n, B, Dp = 256, 4, 4
+    fan_cap = {"shape": f"{B} chains x {Dp} GEMMs {n}^3"}
+    bits_seen = []
+    for plan_label, sched, streams in (("4_streams", G.SchedulePolicy.kChainGreedy, 4),
+                                       ("1_stream", G.SchedulePolicy.kSequential, 1)):
+        cap = {}
+        for label in ("eager", "hip_graph"):
+            g, t = G.gemm_fanout(B, Dp, n)
+            ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList, schedule=sched,
+                            memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=streams)
+            ex.plan()
+            ex.set_input(t["W"], m.fill_random(n * n, 0x4100, -0.0625, 0.0625))
+            for k in range(B):
+                ex.set_input(t["xs"][k], m.fill_random(n * n, 0x4101 + k))
+            if label == "hip_graph":
+                ex.capture()
+            wall = timed_runs(ex, 200)
+            bits_seen.append(np.concatenate([ex.read(o, n * n).view(np.uint32) for o in t["outs"]]))
+            cap[label] = {"us_per_run": round(wall * 1e3, 2)}
+            ex.close()
+        cap["speedup"] = round(cap["eager"]["us_per_run"] / cap["hip_graph"]["us_per_run"], 3)
+        fan_cap[plan_label] = cap
+        log(f"fan-out {B}x{Dp} {n}^3 {plan_label}: eager {cap['eager']['us_per_run']} us, "
+            f"hipGraph {cap['hip_graph']['us_per_run']} us per run")
+    fan_cap["same_bits"] = all(np.array_equal(bits_seen[0], b) for b in bits_seen[1:])
+    out["fanout_small_capture"] = fan_cap
     return out
 
 

@@ -128,17 +128,21 @@ class GraphExecutor {
   [[nodiscard]] Status plan();
   [[nodiscard]] Status set_input(TensorId t, const void* host_data, std::size_t bytes);
   [[nodiscard]] Status run_async();
-  // Captures one iteration of run_async() into a HIP graph (stream capture on
-  // stream 0; the other streams join through the plan's fork/join and
-  // cross-stream events) and instantiates it; every later run_async() replays
-  // that graph with one launch instead of re-issuing the plan's launches and
-  // events.  The reference plans this step as capture_cuda_graph
-  // (include/mcke/graph/executor.hpp:23-27).  Refused with per-node timing probes
-  // (their events would be frozen into the graph), with the vendor-library GEMM
-  // (its internals are not ours to vet for memset nodes), and for plans on more
-  // than one stream (multi-stream capture is switched off).  With
-  // poison_buffers the pattern captured is the capture iteration's.  plan()
-  // drops the captured graph, since it binds the old plan's buffers.
+  // Captures one iteration of run_async() into a HIP graph and instantiates it;
+  // every later run_async() replays that graph with one launch on stream 0
+  // instead of re-issuing the plan's launches and events.  A single-stream plan
+  // is stream-captured whole.  A plan on several streams is assembled node by
+  // node: each node's launches are captured on its own stream into a child
+  // graph, and the child joins the parent graph after the previous node of its
+  // stream and after the nodes that record the events it waits on, so the
+  // graph's edges are exactly the plan's stream order and cross-stream events;
+  // no capture spans two streams.  The reference plans this step as
+  // capture_cuda_graph (include/mcke/graph/executor.hpp:23-27).  Refused with
+  // per-node timing probes (their events would be frozen into the graph) and
+  // with the vendor-library GEMM (its internals are not ours to vet for memset
+  // nodes).  With poison_buffers the pattern captured is the capture
+  // iteration's.  plan() drops the captured graph, since it binds the old plan's
+  // buffers.
   [[nodiscard]] Status capture_graph();
   [[nodiscard]] bool captured() const noexcept { return graph_exec_ != nullptr; }
   [[nodiscard]] Status synchronize();
@@ -161,6 +165,9 @@ class GraphExecutor {
   // streams they were last used on still exist, then drops the plan.
   void release_plan();
   [[nodiscard]] Status issue_plan();   // one iteration's launches, events and fills
+  [[nodiscard]] Status issue_poison(rt::Stream& s0);   // the poison fills of one iteration
+  [[nodiscard]] Status launch_node(std::size_t i, rt::Stream& st);   // scheduled node i's op
+  [[nodiscard]] Status assemble_across_streams(void** out_exec);
   void release_capture();
 
   Graph graph_;
@@ -173,6 +180,9 @@ class GraphExecutor {
   std::vector<std::pair<TensorId, std::vector<char>>> input_cache_;
   bool planned_ = false;
   void* graph_exec_ = nullptr;   // hipGraphExec_t of the captured iteration
+  // hipGraph_t of each node's capture (multi-stream plans), kept until the
+  // executable graph assembled from them is released.
+  std::vector<void*> capture_parts_;
 };
 
 }  // namespace mcke

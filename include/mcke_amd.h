@@ -229,12 +229,9 @@ int mcke_rt_event_query(void* event, int* done);
 int mcke_rt_event_synchronize(void* event);
 int mcke_rt_event_elapsed_ms(void* start, void* stop, float* ms);
 
-/* raw_device_malloc / raw_device_free (device.cpp:104-130): hipMalloc, which is
- * 256-byte aligned; out-of-memory maps to MCKE_STATUS_OUT_OF_MEMORY. */
 /* Stream capture into a HIP graph (no reference counterpart: the reference plans
  * it as capture_cuda_graph, include/mcke/graph/executor.hpp:23-27).  Capture runs
- * in thread-local mode on a stream this library created; other streams join the
- * capture through events recorded on a capturing stream.  end_capture
+ * in thread-local mode on a stream this library created.  end_capture
  * instantiates the captured graph and returns the executable graph; launch
  * replays it on `stream`; destroy releases it.  Nothing captured may be a memset
  * (kernels fill memory here, never hipMemsetAsync). */
@@ -242,6 +239,28 @@ int mcke_rt_stream_begin_capture(void* stream);
 int mcke_rt_stream_end_capture(void* stream, void** out_exec);
 int mcke_rt_graph_launch(void* exec, void* stream);
 int mcke_rt_graph_destroy(void* exec);
+
+/* Explicit graph assembly, for plans on several streams (no reference
+ * counterpart).  Each node's launches are stream-captured on one stream
+ * (end_capture_graph returns the captured, not yet instantiated, hipGraph_t),
+ * then added to a parent graph after the parent nodes given in deps; no capture
+ * ever spans two streams.  add_child adds a child that is a chain of kernel
+ * nodes (what one stream's capture of kernel launches gives) as the same chain
+ * of kernel nodes, an empty child as an empty node and any other child as a
+ * child-graph node; *out_node is the last node added.  The caller keeps the
+ * child until the parent and every executable graph made from it are
+ * released.  instantiate turns the parent into an
+ * executable graph for mcke_rt_graph_launch / mcke_rt_graph_destroy;
+ * graph_release frees a graph that is not instantiated (parent or child). */
+int mcke_rt_stream_end_capture_graph(void* stream, void** out_graph);
+int mcke_rt_graph_create(void** out_graph);
+int mcke_rt_graph_add_child(void* graph, void* child, void* const* deps, size_t n_deps,
+                            void** out_node);
+int mcke_rt_graph_instantiate(void* graph, void** out_exec);
+int mcke_rt_graph_release(void* graph);
+
+/* raw_device_malloc / raw_device_free (device.cpp:104-130): hipMalloc, which is
+ * 256-byte aligned; out-of-memory maps to MCKE_STATUS_OUT_OF_MEMORY. */
 int mcke_rt_malloc(void** out_ptr, size_t bytes);
 int mcke_rt_free(void* ptr);
 int mcke_rt_host_alloc(void** out_ptr, size_t bytes); /* pinned host memory */

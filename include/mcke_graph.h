@@ -125,9 +125,11 @@ int mcke_executor_run_async(mcke_executor* e);
 int mcke_executor_synchronize(mcke_executor* e);
 /* Captures one iteration of the plan into a HIP graph; later run_async calls replay
  * it with one launch (GraphExecutor::capture_graph; the reference plans this as
- * capture_cuda_graph, executor.hpp:23-27).  FAILED_PRECONDITION with per-node
- * timing probes, a vendor-library GEMM node, or a plan on more than one stream.
- * A new plan() drops the capture. */
+ * capture_cuda_graph, executor.hpp:23-27).  A plan on several streams is
+ * assembled from one single-stream capture per node, with the plan's stream order
+ * and cross-stream events as the graph's edges.  FAILED_PRECONDITION with
+ * per-node timing probes or a vendor-library GEMM node.  A new plan() drops the
+ * capture. */
 int mcke_executor_capture(mcke_executor* e);
 int mcke_executor_is_captured(mcke_executor* e, int* out);
 /* Copies tensor t (an output, or any tensor with a buffer) to host memory and waits. */

@@ -185,6 +185,99 @@ int mcke_rt_graph_destroy(void* exec) {
   return ok();
 }
 
+int mcke_rt_stream_end_capture_graph(void* stream, void** out_graph) {
+  if (!stream || !out_graph) return invalid("mcke_rt_stream_end_capture_graph: null argument");
+  *out_graph = nullptr;
+  hipGraph_t graph = nullptr;
+  MCKE_HIP_TRY(hipStreamEndCapture(static_cast<hipStream_t>(stream), &graph));
+  *out_graph = graph;
+  return ok();
+}
+
+int mcke_rt_graph_create(void** out_graph) {
+  if (!out_graph) return invalid("mcke_rt_graph_create: null out");
+  *out_graph = nullptr;
+  hipGraph_t graph = nullptr;
+  MCKE_HIP_TRY(hipGraphCreate(&graph, 0));
+  *out_graph = graph;
+  return ok();
+}
+
+int mcke_rt_graph_add_child(void* graph, void* child, void* const* deps, size_t n_deps,
+                            void** out_node) {
+  if (!graph || !child || !out_node || (n_deps > 0 && !deps))
+    return invalid("mcke_rt_graph_add_child: null argument");
+  *out_node = nullptr;
+  std::vector<hipGraphNode_t> dep(n_deps);
+  for (size_t i = 0; i < n_deps; ++i) {
+    if (!deps[i]) return invalid("mcke_rt_graph_add_child: null dependency");
+    dep[i] = static_cast<hipGraphNode_t>(deps[i]);
+  }
+  hipGraph_t parent = static_cast<hipGraph_t>(graph);
+  hipGraph_t sub = static_cast<hipGraph_t>(child);
+  size_t n_nodes = 0;
+  MCKE_HIP_TRY(hipGraphGetNodes(sub, nullptr, &n_nodes));
+  hipGraphNode_t node = nullptr;
+  if (n_nodes == 0) {
+    MCKE_HIP_TRY(hipGraphAddEmptyNode(&node, parent, dep.data(), n_deps));
+    *out_node = node;
+    return ok();
+  }
+  // A child captured from one stream is a chain of kernel nodes: walk it from its
+  // root and add each kernel straight into the parent after the previous one, so
+  // the parent holds plain kernel nodes.  Anything else is nested as a child
+  // graph node.
+  std::vector<hipGraphNode_t> chain;
+  size_t n_roots = 0;
+  MCKE_HIP_TRY(hipGraphGetRootNodes(sub, nullptr, &n_roots));
+  if (n_roots == 1) {
+    hipGraphNode_t cur = nullptr;
+    MCKE_HIP_TRY(hipGraphGetRootNodes(sub, &cur, &n_roots));
+    while (cur && chain.size() < n_nodes) {
+      hipGraphNodeType type;
+      MCKE_HIP_TRY(hipGraphNodeGetType(cur, &type));
+      if (type != hipGraphNodeTypeKernel) break;
+      chain.push_back(cur);
+      size_t n_next = 0;
+      MCKE_HIP_TRY(hipGraphNodeGetDependentNodes(cur, nullptr, &n_next));
+      if (n_next > 1) break;
+      hipGraphNode_t next = nullptr;
+      if (n_next == 1) MCKE_HIP_TRY(hipGraphNodeGetDependentNodes(cur, &next, &n_next));
+      cur = next;
+    }
+  }
+  if (chain.size() == n_nodes) {
+    const hipGraphNode_t* prev = dep.data();
+    size_t n_prev = n_deps;
+    for (hipGraphNode_t k : chain) {
+      hipKernelNodeParams kp{};
+      MCKE_HIP_TRY(hipGraphKernelNodeGetParams(k, &kp));
+      MCKE_HIP_TRY(hipGraphAddKernelNode(&node, parent, prev, n_prev, &kp));
+      prev = &node;
+      n_prev = 1;
+    }
+  } else {
+    MCKE_HIP_TRY(hipGraphAddChildGraphNode(&node, parent, dep.data(), n_deps, sub));
+  }
+  *out_node = node;
+  return ok();
+}
+
+int mcke_rt_graph_instantiate(void* graph, void** out_exec) {
+  if (!graph || !out_exec) return invalid("mcke_rt_graph_instantiate: null argument");
+  *out_exec = nullptr;
+  hipGraphExec_t exec = nullptr;
+  MCKE_HIP_TRY(hipGraphInstantiate(&exec, static_cast<hipGraph_t>(graph), nullptr, nullptr, 0));
+  *out_exec = exec;
+  return ok();
+}
+
+int mcke_rt_graph_release(void* graph) {
+  if (!graph) return ok();
+  MCKE_HIP_TRY(hipGraphDestroy(static_cast<hipGraph_t>(graph)));
+  return ok();
+}
+
 int mcke_rt_event_create(void** out_event, int timing) {
   if (!out_event) return invalid("mcke_rt_event_create: null out");
   hipEvent_t e = nullptr;

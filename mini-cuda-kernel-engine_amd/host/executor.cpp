@@ -183,19 +183,14 @@ Status GraphExecutor::set_input(TensorId t, const void* host_data, std::size_t b
 void GraphExecutor::release_capture() {
   if (graph_exec_) (void)mcke_rt_graph_destroy(graph_exec_);
   graph_exec_ = nullptr;
+  for (void* g : capture_parts_) (void)mcke_rt_graph_release(g);
+  capture_parts_.clear();
 }
 
 Status GraphExecutor::capture_graph() {
   if (!planned_) return FailedPreconditionError("capture_graph: call plan() first");
   if (opts_.profile)
     return FailedPreconditionError("capture_graph: per-node timing probes cannot be captured (profile = false)");
-  // Multi-stream capture (the other streams joining through the fork event) ended
-  // in a host segmentation fault inside the HIP runtime on its first run; no cause
-  // in this code has been shown, so that path stays switched off: only plans on
-  // one stream are captured.
-  if (plan_.streams_.size() > 1)
-    return FailedPreconditionError("capture_graph: only single-stream plans are captured (this plan uses " +
-                                   std::to_string(plan_.streams_.size()) + " streams)");
   for (const ScheduledNode& sn : plan_.sched_)
     if (const auto* g = dynamic_cast<const GemmOp*>(graph_.node_op(sn.node)))
       if (g->params().variant == kernels::GemmVariant::kCublasRef)
@@ -204,14 +199,87 @@ Status GraphExecutor::capture_graph() {
   release_capture();
   // Nothing may still be queued on the plan's streams when capture starts.
   for (rt::Stream& st : plan_.streams_) MCKE_RETURN_IF_ERROR(st.synchronize());
-  rt::Stream& s0 = plan_.streams_.front();
-  MCKE_RETURN_IF_ERROR(rc_status(mcke_rt_stream_begin_capture(s0.native()), "capture_graph: begin"));
-  const Status issued = issue_plan();
   void* exec = nullptr;
-  const Status ended = rc_status(mcke_rt_stream_end_capture(s0.native(), &exec), "capture_graph: end");
-  MCKE_RETURN_IF_ERROR(issued);
-  MCKE_RETURN_IF_ERROR(ended);
+  if (plan_.streams_.size() > 1) {
+    MCKE_RETURN_IF_ERROR(assemble_across_streams(&exec));
+  } else {
+    rt::Stream& s0 = plan_.streams_.front();
+    MCKE_RETURN_IF_ERROR(rc_status(mcke_rt_stream_begin_capture(s0.native()), "capture_graph: begin"));
+    const Status issued = issue_plan();
+    const Status ended = rc_status(mcke_rt_stream_end_capture(s0.native(), &exec), "capture_graph: end");
+    if (!issued.ok() && exec) (void)mcke_rt_graph_destroy(exec);
+    MCKE_RETURN_IF_ERROR(issued);
+    MCKE_RETURN_IF_ERROR(ended);
+  }
   graph_exec_ = exec;
+  return OkStatus();
+}
+
+namespace {
+// Owns a hipGraph_t that is not instantiated (the parent or a child).
+struct GraphHolder {
+  void* g = nullptr;
+  GraphHolder() = default;
+  GraphHolder(const GraphHolder&) = delete;
+  GraphHolder& operator=(const GraphHolder&) = delete;
+  ~GraphHolder() {
+    if (g) (void)mcke_rt_graph_release(g);
+  }
+};
+}  // namespace
+
+Status GraphExecutor::assemble_across_streams(void** out_exec) {
+  *out_exec = nullptr;
+  // On failure the parts captured so far go with the next release_capture().
+  GraphHolder parent;
+  MCKE_RETURN_IF_ERROR(rc_status(mcke_rt_graph_create(&parent.g), "capture_graph: create"));
+  // Captures what `issue` enqueues on `st` into a child graph and adds it to the
+  // parent after `deps`; *node is the new parent node.
+  auto add_captured = [&](rt::Stream& st, const std::vector<void*>& deps, auto&& issue,
+                          void** node) -> Status {
+    MCKE_RETURN_IF_ERROR(rc_status(mcke_rt_stream_begin_capture(st.native()), "capture_graph: begin"));
+    const Status issued = issue();
+    void* child = nullptr;
+    const Status ended =
+        rc_status(mcke_rt_stream_end_capture_graph(st.native(), &child), "capture_graph: end");
+    if (child) capture_parts_.push_back(child);
+    MCKE_RETURN_IF_ERROR(issued);
+    MCKE_RETURN_IF_ERROR(ended);
+    return rc_status(mcke_rt_graph_add_child(parent.g, child, deps.data(), deps.size(), node),
+                     "capture_graph: add node");
+  };
+  rt::Stream& s0 = plan_.streams_.front();
+  // The poison fills come first: every node without another dependency waits on them.
+  void* prologue = nullptr;
+  if (opts_.poison_buffers && plan_.arena_)
+    MCKE_RETURN_IF_ERROR(add_captured(s0, {}, [&] { return issue_poison(s0); }, &prologue));
+  std::vector<void*> last_on_stream(plan_.streams_.size(), nullptr);
+  std::vector<void*> recorded_by(plan_.events_.size(), nullptr);
+  for (std::size_t i = 0; i < plan_.sched_.size(); ++i) {
+    const ScheduledNode& sn = plan_.sched_[i];
+    std::vector<void*> deps;
+    auto add_dep = [&](void* d) {
+      if (d && std::find(deps.begin(), deps.end(), d) == deps.end()) deps.push_back(d);
+    };
+    add_dep(last_on_stream[sn.stream_idx]);
+    for (std::uint32_t w = 0; w < sn.wait_count; ++w) {
+      const std::size_t ev = plan_.wait_pool_[sn.wait_offset + w];
+      // The plan was verified to record every event before its first wait in
+      // issue order, so its recording node is already in the graph.
+      if (ev >= recorded_by.size() || !recorded_by[ev])
+        return InternalError("capture_graph: node '" + graph_.node(sn.node).name +
+                             "' waits on an event no earlier node records");
+      add_dep(recorded_by[ev]);
+    }
+    if (deps.empty()) add_dep(prologue);
+    rt::Stream& st = plan_.streams_[sn.stream_idx];
+    void* node = nullptr;
+    MCKE_RETURN_IF_ERROR(add_captured(st, deps, [&] { return launch_node(i, st); }, &node));
+    last_on_stream[sn.stream_idx] = node;
+    if (sn.record_event != kNoEvent) recorded_by[sn.record_event] = node;
+  }
+  MCKE_RETURN_IF_ERROR(
+      rc_status(mcke_rt_graph_instantiate(parent.g, out_exec), "capture_graph: instantiate"));
   return OkStatus();
 }
 
@@ -227,26 +295,42 @@ Status GraphExecutor::run_async() {
   return issue_plan();
 }
 
+Status GraphExecutor::issue_poison(rt::Stream& s0) {
+  if (!opts_.poison_buffers || !plan_.arena_) return OkStatus();
+  // A different finite pattern each iteration, everywhere but the inputs: a
+  // node that reads bytes nobody wrote this iteration gets a changing value,
+  // which the numerics gate sees as run-to-run variance.
+  const std::uint32_t pat = opts_.poison_pattern + static_cast<std::uint32_t>(plan_.iteration_) * 0x9E3779B9u;
+  char* base = static_cast<char*>(plan_.arena_->data());
+  std::size_t cursor = 0;
+  auto poison = [&](std::size_t lo, std::size_t hi) -> Status {
+    if (hi <= lo) return OkStatus();
+    return rc_status(mcke_fill_u32_async(base + lo, pat, (hi - lo) / 4, s0.native()), "poison");
+  };
+  for (const auto& r : plan_.input_byte_ranges_) {
+    MCKE_RETURN_IF_ERROR(poison(cursor, r.first));
+    cursor = r.second;
+  }
+  return poison(cursor, plan_.arena_->bytes());
+}
+
+Status GraphExecutor::launch_node(std::size_t i, rt::Stream& st) {
+  const ScheduledNode& sn = plan_.sched_[i];
+  OpContext ctx;
+  ctx.stream = st.native();
+  ctx.device = &device_;
+  if (sn.stream_idx < plan_.workspaces_.size() && plan_.workspaces_[sn.stream_idx]) {
+    ctx.workspace = plan_.workspaces_[sn.stream_idx]->data();
+    ctx.workspace_bytes = plan_.workspaces_[sn.stream_idx]->bytes();
+  }
+  NvtxRange range(graph_.node(sn.node).name.c_str());
+  return graph_.node_op(sn.node)->launch(ctx, plan_.node_inputs_[i], plan_.node_outputs_[i]);
+}
+
 Status GraphExecutor::issue_plan() {
   const std::size_t K = plan_.streams_.size();
   rt::Stream& s0 = plan_.streams_.front();
-  if (opts_.poison_buffers && plan_.arena_) {
-    // A different finite pattern each iteration, everywhere but the inputs: a
-    // node that reads bytes nobody wrote this iteration gets a changing value,
-    // which the numerics gate sees as run-to-run variance.
-    const std::uint32_t pat = opts_.poison_pattern + static_cast<std::uint32_t>(plan_.iteration_) * 0x9E3779B9u;
-    char* base = static_cast<char*>(plan_.arena_->data());
-    std::size_t cursor = 0;
-    auto poison = [&](std::size_t lo, std::size_t hi) -> Status {
-      if (hi <= lo) return OkStatus();
-      return rc_status(mcke_fill_u32_async(base + lo, pat, (hi - lo) / 4, s0.native()), "poison");
-    };
-    for (const auto& r : plan_.input_byte_ranges_) {
-      MCKE_RETURN_IF_ERROR(poison(cursor, r.first));
-      cursor = r.second;
-    }
-    MCKE_RETURN_IF_ERROR(poison(cursor, plan_.arena_->bytes()));
-  }
+  MCKE_RETURN_IF_ERROR(issue_poison(s0));
   if (K > 1) {
     MCKE_RETURN_IF_ERROR(plan_.fork_event_[0].record(s0));
     for (std::size_t s = 1; s < K; ++s) MCKE_RETURN_IF_ERROR(plan_.streams_[s].wait(plan_.fork_event_[0]));
@@ -257,19 +341,9 @@ Status GraphExecutor::issue_plan() {
     rt::Stream& st = plan_.streams_[sn.stream_idx];
     for (std::uint32_t w = 0; w < sn.wait_count; ++w)
       MCKE_RETURN_IF_ERROR(st.wait(plan_.events_[plan_.wait_pool_[sn.wait_offset + w]]));
-    OpContext ctx;
-    ctx.stream = st.native();
-    ctx.device = &device_;
-    if (sn.stream_idx < plan_.workspaces_.size() && plan_.workspaces_[sn.stream_idx]) {
-      ctx.workspace = plan_.workspaces_[sn.stream_idx]->data();
-      ctx.workspace_bytes = plan_.workspaces_[sn.stream_idx]->bytes();
-    }
     const std::size_t p = (i * static_cast<std::size_t>(plan_.probe_slots_) + static_cast<std::size_t>(slot)) * 2;
     if (opts_.profile) MCKE_RETURN_IF_ERROR(plan_.probes_[p].record(st));
-    {
-      NvtxRange range(graph_.node(sn.node).name.c_str());
-      MCKE_RETURN_IF_ERROR(graph_.node_op(sn.node)->launch(ctx, plan_.node_inputs_[i], plan_.node_outputs_[i]));
-    }
+    MCKE_RETURN_IF_ERROR(launch_node(i, st));
     if (opts_.profile) MCKE_RETURN_IF_ERROR(plan_.probes_[p + 1].record(st));
     if (sn.record_event != kNoEvent) MCKE_RETURN_IF_ERROR(plan_.events_[sn.record_event].record(st));
   }

@@ -228,14 +228,19 @@ def test_captured_replays_match_eager(G, orc, poison):
     ex.close()
 
 
-@pytest.mark.skip(reason="multi-stream capture is switched off: its one run ended in a host "
-                         "segfault inside the HIP runtime, cause not shown in this code")
-def test_captured_fanout_across_streams(G, orc):
+@pytest.mark.parametrize("schedule,poison", [("kLevelParallel", False), ("kChainGreedy", True)])
+def test_captured_fanout_across_streams(G, orc, schedule, poison):
+    """A plan on several streams is assembled into one graph (one child graph per
+    node, edges from stream order and cross-stream events).  Every replay, with
+    the program's own eager work and synchronisations between replays, gives the
+    eager bits, and the eager bits match the oracle chain of GEMMs."""
+    import mcke_amd as m
     n, B, Dp = 128, 4, 3
     g, t = G.gemm_fanout(B, Dp, n)
-    ex = G.Executor(g, schedule=G.SchedulePolicy.kLevelParallel,
-                    memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4)
+    ex = G.Executor(g, schedule=getattr(G.SchedulePolicy, schedule),
+                    memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4, poison_buffers=poison)
     ex.plan()
+    assert ex.plan_info()["num_streams_used"] > 1
     w = (orc.fill_random(n * n, 7) * 0.0625).astype(np.float32)
     xs = [orc.fill_random(n * n, 300 + k) for k in range(B)]
     ex.set_input(t["W"], w)
@@ -244,11 +249,27 @@ def test_captured_fanout_across_streams(G, orc):
     ex.run_sync()
     eager = [ex.read(t["outs"][k], n * n) for k in range(B)]
     ex.capture()
-    for rep in range(3):
+    assert ex.captured
+    scratch_x = m.DeviceBuffer.from_array(orc.fill_normal(4096, 9))
+    scratch_y = m.DeviceBuffer(4096 * 4)
+    for rep in range(4):
         ex.run_sync()
         for k in range(B):
             got = ex.read(t["outs"][k], n * n)
             assert np.array_equal(got.view(np.uint32), eager[k].view(np.uint32)), (rep, k)
+        m.launch_activation_f32(scratch_x, scratch_y, 4096, m.Activation.kGeluTanh, 4).throw_if_error()
+        m.device_synchronize()
+    # new inputs are seen by the replays
+    xs2 = [orc.fill_random(n * n, 900 + k) for k in range(B)]
+    for k in range(B):
+        ex.set_input(t["xs"][k], xs2[k])
+    ex.run_sync()
+    for k in range(B):
+        want = xs2[k]
+        for _ in range(Dp):
+            want = orc.gemm(want, w, np.zeros(n * n, np.float32), n, n, n)
+        r = orc.compare(ex.read(t["outs"][k], n * n), want, 1e-4, 1e-5)
+        assert r.ok, f"replay with new inputs, branch {k}: {r}"
     for k in range(B):
         want = xs[k]
         for _ in range(Dp):
@@ -258,16 +279,37 @@ def test_captured_fanout_across_streams(G, orc):
     ex.close()
 
 
-def test_capture_refused_for_multi_stream_plans(G):
-    """The refusal is checked on the host before any capture call is made."""
-    g, _ = G.gemm_fanout(4, 2, 64)
-    ex = G.Executor(g, schedule=G.SchedulePolicy.kChainGreedy, num_streams=4)
+def test_captured_diamond_with_workspace_reduce(G, orc):
+    """A GEMM feeding three branches (bias+GELU -> softmax, a two-pass row sum
+    that uses its stream's workspace, a row max) on several streams, with
+    poisoning: every replay of the assembled graph gives the eager bits."""
+    T, D, F = 256, 128, 512
+    g = G.Graph()
+    x = g.add_input((T, D), "x")
+    w1 = g.add_input((D, F), "W1")
+    b1 = g.add_input((F,), "b1")
+    g1 = g.add_gemm(x, w1, "gemm1")
+    h = g.add_bias_act(g1, b1, "bias_gelu", act=3)
+    y = g.add_softmax(h, "softmax")
+    rs = g.add_reduce(g1, "row_sum", kind=0, variant=2)
+    rm = g.add_reduce(g1, "row_max", kind=1, variant=1)
+    for o in (y, rs, rm):
+        g.mark_output(o)
+    ex = G.Executor(g, schedule=G.SchedulePolicy.kLevelParallel,
+                    memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=3, poison_buffers=True)
     ex.plan()
-    assert ex.plan_info()["num_streams_used"] == 4
-    with pytest.raises(Exception, match="single-stream"):
-        ex.capture()
-    assert not ex.captured
-    ex.run_sync()                          # the eager path is unaffected
+    assert ex.plan_info()["num_streams_used"] > 1
+    ex.set_input(x, orc.fill_normal(T * D, 11, 0.0, 1.0))
+    ex.set_input(w1, orc.fill_normal(D * F, 12, 0.0, 0.05))
+    ex.set_input(b1, orc.fill_normal(F, 13, 0.0, 0.01))
+    ex.run_sync()
+    outs = ((y, T * F), (rs, T), (rm, T))
+    eager = [ex.read(o, n) for o, n in outs]
+    ex.capture()
+    for rep in range(3):
+        ex.run_sync()
+        for (o, n), want in zip(outs, eager):
+            assert np.array_equal(ex.read(o, n).view(np.uint32), want.view(np.uint32)), (rep, o)
     ex.close()
 
 
