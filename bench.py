@@ -690,11 +690,17 @@ def graph_section(m, steps=5, warmup=2):
     return out
 
 
-def cpu_baseline(m, gemm_bufs, seconds_target=12.0):
+def cpu_baseline(m, gemm_bufs, seconds_target=12.0, stream=None):
     """The CPU reference GEMM (reference tests/reference.hpp:199-211: i-j-p loops,
     double accumulation, one thread) on a row slab of the same 8192^3 problem,
     and a parity check of the GPU's C on that slab.  Uses oracle/_ref (the
-    reference's own code) when it was built, else the plain-C restatement."""
+    reference's own code) when it was built, else the plain-C restatement.
+
+    Beside it: the full reference at 512^3 and 1024^3 (configs[0]'s smallest
+    sweep sizes) against the GPU's C at those sizes, and the same row-slab work
+    split by rows over the host cores (one reference call per thread; ctypes
+    releases the GIL), reported as a separate figure."""
+    import concurrent.futures
     import oracle
 
     a, b, c, n = gemm_bufs
@@ -725,16 +731,59 @@ def cpu_baseline(m, gemm_bufs, seconds_target=12.0):
     got = hc[:rows_done * n]
     r = oracle.compare(got, want, oracle.tol_gemm(n), oracle.abs_tol_gemm(n))
     flops = 2.0 * rows_done * n * n
+    ref_gemm = oracle.Ref.gemm if use_ref else oracle.gemm
+
+    # The full reference at 512^3 and 1024^3, on bench inputs of those sizes.
+    full = []
+    D = m.DeviceBuffer
+    for nn in (512, 1024):
+        fa, fb = m.fill_random(nn * nn, 0x6E33A), m.fill_random(nn * nn, 0x8B10C)
+        da, db, dc = D.from_array(fa), D.from_array(fb), D.zeros(nn * nn)
+        m.launch_gemm_f32(da, db, dc, nn, nn, nn, 1.0, 0.0, m.GemmVariant.kMfmaF32,
+                          m.gemm_mfma_default_tile(nn, nn, nn), stream).throw_if_error()
+        gpu_c = dc.download(nn * nn, stream=stream)
+        t = time.perf_counter()
+        want_full = ref_gemm(fa, fb, np.zeros(nn * nn, np.float32), nn, nn, nn, 1.0, 0.0)
+        dt = time.perf_counter() - t
+        rf = oracle.compare(gpu_c, want_full, oracle.tol_gemm(nn), oracle.abs_tol_gemm(nn))
+        full.append({"n": nn, "seconds": round(dt, 3), "tflops": round(2.0 * nn ** 3 / dt / 1e12, 6),
+                     "parity_of_gpu_c": {"ok": bool(rf.ok), "max_abs_err": rf.max_abs_err,
+                                         "max_rel_err": rf.max_rel_err,
+                                         "check": "every element, rel tol_gemm + abs abs_tol_gemm"}})
+        log(f"cpu baseline: full reference {nn}^3 in {dt:.2f} s; GPU C "
+            f"{'matches' if rf.ok else 'DIFFERS'}")
+        del da, db, dc
+
+    # Row-parallel: the next rows of the same 8192^3 problem, one row per thread,
+    # on the host cores this process may use (at most 16, the GPU box's share).
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    r0 = rows_done
+    def one_row(i):
+        row = r0 + i
+        return ref_gemm(ha[row * n:(row + 1) * n], hb, np.zeros(n, np.float32), 1, n, n, 1.0, 0.0)
+    t = time.perf_counter()
+    with concurrent.futures.ThreadPoolExecutor(threads) as pool:
+        par_rows = list(pool.map(one_row, range(threads)))
+    dt_par = time.perf_counter() - t
+    rp = oracle.compare(hc[r0 * n:(r0 + threads) * n], np.concatenate(par_rows),
+                        oracle.tol_gemm(n), oracle.abs_tol_gemm(n))
+    log(f"cpu baseline: row-parallel, {threads} threads: {threads} rows in {dt_par:.1f} s")
     return {
         "value": round(flops / elapsed / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
         "kind": kind,
         "sample": f"rows 0..{rows_done - 1} of C for the 8192^3 GEMM ({rows_done}x8192x8192, "
                   f"{elapsed:.1f} s, 1 thread of {os.cpu_count()} host cores, double "
                   f"accumulation in the reference's i-j-p order)",
+        "extrapolated_8192_s": round(elapsed / rows_done * n, 1),
         "parity_on_sample": {"ok": bool(r.ok), "max_abs_err": r.max_abs_err,
                              "max_rel_err": r.max_rel_err,
                              "tol": f"rel tol_gemm(8192)={oracle.tol_gemm(n):.3g} + abs "
                                     f"abs_tol_gemm(8192)={oracle.abs_tol_gemm(n):.3g}"},
+        "full_reference": full,
+        "row_parallel": {"threads": threads, "rows": f"{r0}..{r0 + threads - 1}",
+                         "seconds": round(dt_par, 2),
+                         "tflops": round(2.0 * threads * n * n / dt_par / 1e12, 6),
+                         "parity_ok": bool(rp.ok)},
     }
 
 
@@ -818,7 +867,7 @@ def main(argv=None) -> int:
                 f"({time.perf_counter() - t0:.1f} s)")
     if not args.no_cpu and gemm_bufs[0] is not None:
         log(f"cpu baseline: reference GEMM on a row slab (~{args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline(m, gemm_bufs, args.cpu_seconds)
+        cpu = cpu_baseline(m, gemm_bufs, args.cpu_seconds, stream)
         log(f"cpu baseline: {cpu['value']} TFLOP/s ({cpu['sample']})")
     summaries = [op.summary(s["measured_peak"] if "measured_peak" in s else None,
                             s.get("hbm_traffic_bytes")) for op, s in zip(ops, summaries)]

@@ -456,6 +456,7 @@ struct LpDmaShape {
   static constexpr int MT = BM / 64, NT = BN / 64;       // MFMA tiles per wave
   static constexpr int kMfmas = MT * NT;                 // per sub-step
   static constexpr int kReads = MT + 2 * NT;             // fragment reads per sub-step
+  static constexpr int kReadSpan = kMfmas;               // reads go after the first kReadSpan MFMAs
   static_assert(BN == 128 || BN == 256, "B rows of 16 or 32 chunks");
   static_assert(kABytes % 4096 == 0 && kBBytes % 4096 == 0, "stage must split over 4 waves");
   static_assert(STAGES >= 3 && (STAGES - 2) * L <= 63, "vmcnt counts at most 63 loads");
@@ -515,9 +516,9 @@ __device__ __forceinline__ void lp_dma_slot(f32x16 (&acc)[BM / 64][BN / 64],
   if constexpr (TRANS) acc[i][j] = LpMfma<T>::run(b, cav[i], acc[i][j]);
   else acc[i][j] = LpMfma<T>::run(cav[i], b, acc[i][j]);
   __builtin_amdgcn_sched_barrier(0);
-  // Reads RR with RR * kMfmas / kReads == IDX go after this MFMA.
+  // Reads RR with RR * kReadSpan / kReads == IDX go after this MFMA.
   [&]<int... RR>(std::integer_sequence<int, RR...>) {
-    ((RR * S::kMfmas / S::kReads == IDX
+    ((RR * S::kReadSpan / S::kReads == IDX
           ? S::template read_one<SUB, RR>(st, a_off, b_off, nav, nbv)
           : void()),
      ...);
