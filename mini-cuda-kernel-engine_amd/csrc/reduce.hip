@@ -9,11 +9,14 @@
 //                classic LDS tree (1 + log2(256) = 9 barriers);
 //   kWarpShuffle one workgroup per row; wave64 butterfly, then one LDS stage
 //                across the 4 waves (1 barrier);
-//   kTwoPass     (rows x split) workgroups write partials to the caller's
-//                workspace, then one workgroup per row combines them in a fixed
-//                order.  With rows == 1 this is the full-tensor reduction.
-// Every variant is deterministic (no atomics): the same input gives the same
-// bits on every run.
+//   kTwoPass     (rows x split) workgroups reduce column chunks of a row to
+//                partials in the caller's workspace; the workgroup that
+//                finishes a row last (an arrival counter per row) folds that
+//                row's partials in a fixed order and writes out[r], all in one
+//                launch.  With rows == 1 this is the full-tensor reduction.
+// Every variant is deterministic: no value is combined atomically (the only
+// atomic is kTwoPass's arrival count), so the same input gives the same bits on
+// every run.
 //
 // The row sweep: 256 lanes walk the row in 16-byte (float4) steps when the row
 // starts are 16-byte aligned, four loads in flight per lane before any add.
@@ -22,8 +25,10 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <mutex>
 #include <string>
 #include <type_traits>
+#include <unordered_map>
 
 #include "common.hpp"
 #include "device_math.hpp"
@@ -33,16 +38,29 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kLoadUnroll = 4;      // loads in flight per lane, one-pass kernels
-constexpr int kPass1Unroll = 8;     // loads in flight per lane, kTwoPass pass 1
 // kTwoPass sizing: one workgroup per CU on a 256-CU part, each lane keeping 8
-// float4 loads in flight.  Measured on the full-tensor sum of 2^26 floats
-// (pass 1 + pass 2): 42.1 us at 256 x 8, 42.3 us at 512 x 4, 43.6 us at
-// 1024 x 4, 45.5 us at 2048 x 4 -- more workgroups buy nothing in pass 1 and
-// cost pass 2.  A workgroup never gets fewer than kMinColsPerBlock columns of
-// one row.
+// float4 loads in flight.  Measured on the full-tensor sum of 2^26 floats (one
+// launch, fold by the last arrival): 41.0 us at 256 x 8, 42.5 us at 512 x 8,
+// 44.9 us at 1024 x 8, 50.3 us at 2048 x 8, and 54.5 us at 256 x 4 -- each
+// workgroup ends with a round trip (its partial's store, then the arrival
+// count) during which its slot issues no loads, so fewer, longer workgroups win.
+constexpr int kPass1Unroll = 8;
 constexpr int64_t kTargetBlocks = 256;
 constexpr int64_t kMinColsPerBlock = 4096;
 constexpr int64_t kMaxSplit = 65535;
+
+// Arrival counters of kTwoPass rows, owned by the library (zero when the code
+// object loads).  A launch takes the block of kCountersPerBlock counters that
+// belongs to its stream, one counter per row.  Launches on one stream run one
+// after another -- and a captured graph keeps the order of the nodes captured
+// on one stream -- so two launches that run at the same time never share a
+// counter.  Every counter is zero at rest: the workgroup that arrives last on a
+// row resets it.  Launches with more rows than a block holds, or on a stream
+// beyond the first kCounterBlocks seen, fall back to two launches (partials,
+// then a one-workgroup-per-row fold) and use no counter.
+constexpr int kCounterBlocks = 1024;
+constexpr int kCountersPerBlock = 256;
+__device__ unsigned int g_row_arrivals[kCounterBlocks * kCountersPerBlock];
 
 struct SumOp {
   static __device__ __forceinline__ float identity() { return 0.0f; }
@@ -134,12 +152,59 @@ __global__ __launch_bounds__(kThreads) void row_reduce_kernel(const float* __res
   if (threadIdx.x == 0) out[r] = MEAN ? v / static_cast<float>(cols) : v;
 }
 
-// Pass 1: workgroup (s, r) reduces columns [s*chunk, min(cols, (s+1)*chunk)) of
-// row r into ws[r*split + s].
-template <class Op, bool VEC>
-__global__ __launch_bounds__(kThreads) void row_reduce_pass1_kernel(
-    const float* __restrict__ x, float* __restrict__ ws, int64_t cols, int64_t chunk,
-    int64_t split) {
+// Folds the `split` partials p[0, split) of one row in a fixed order (lane-
+// strided, then a wave64 butterfly, then the 4 waves in order); the result is
+// valid in thread 0.  Sums are carried in double: the partials are few and this
+// stage should not add error on top of the first.  COHERENT reads the partials
+// with device-scope loads (they were written by other workgroups of the same
+// launch, possibly on another XCD, whose L2 this one does not share).
+template <class Op, bool MEAN, bool COHERENT>
+__device__ __forceinline__ float fold_partials(const float* p, int64_t split, int64_t cols) {
+  auto get = [&](int64_t i) -> float {
+    if constexpr (COHERENT)
+      return __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      return p[i];
+  };
+  const int w = threadIdx.x / kWave;
+  if constexpr (std::is_same_v<Op, SumOp>) {
+    __shared__ double part[kThreads / kWave];
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < split; i += kThreads) acc += static_cast<double>(get(i));
+#pragma unroll
+    for (int m = kWave / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+    if ((threadIdx.x % kWave) == 0) part[w] = acc;
+    __syncthreads();
+    double t = part[0];
+#pragma unroll
+    for (int i = 1; i < kThreads / kWave; ++i) t += part[i];
+    return static_cast<float>(MEAN ? t / static_cast<double>(cols) : t);
+  } else {
+    float acc = Op::identity();
+    for (int64_t i = threadIdx.x; i < split; i += kThreads) acc = Op::apply(acc, get(i));
+    return block_combine_shfl<Op>(acc);
+  }
+}
+
+// kTwoPass, workgroup (s, r): reduces columns [s*chunk, min(cols, (s+1)*chunk))
+// of row r.  With split == 1 the workgroup owns the row and writes out[r].
+// Otherwise it stores its partial to ws[r*split + s]; with a counter block
+// (counter_base >= 0) it then counts its arrival on row r, and the workgroup
+// that arrives last folds the row's partials into out[r].  Without a counter
+// block, out[] is left to row_reduce_fold_kernel.
+//
+// Ordering.  The partial is stored at device scope (a write-through store that
+// bypasses this XCD's L2), and the workgroup waits for that store to complete
+// before it counts its arrival, so every partial counted before the last
+// arrival is already at the device's point of coherence; the fold reads them
+// with device-scope loads that bypass the L2 as well.  The counter add itself is
+// relaxed: an acquire-release add here costs an L2 writeback and invalidate per
+// workgroup (measured: the launch takes 49 us instead of 41 us at 256
+// workgroups), and only the partial needs publishing.
+template <class Op, bool VEC, bool MEAN>
+__global__ __launch_bounds__(kThreads) void row_reduce_split_kernel(
+    const float* __restrict__ x, float* __restrict__ ws, float* __restrict__ out, int64_t cols,
+    int64_t chunk, int64_t split, int counter_base) {
   const int64_t s = blockIdx.x;
   const int64_t r = blockIdx.y;
   const int64_t begin = s * chunk;
@@ -148,39 +213,53 @@ __global__ __launch_bounds__(kThreads) void row_reduce_pass1_kernel(
   float v = Op::identity();
   if (begin < end) v = thread_partial<Op, VEC, kPass1Unroll>(x + r * cols, begin, end);
   v = block_combine_shfl<Op>(v);
-  if (threadIdx.x == 0) ws[r * split + s] = v;
+  if (split == 1) {
+    if (threadIdx.x == 0) out[r] = MEAN ? v / static_cast<float>(cols) : v;
+    return;
+  }
+  __shared__ int last;
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(ws + r * split + s, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int is_last = 0;
+    if (counter_base >= 0) {
+      unsigned int* cnt = g_row_arrivals + counter_base + r;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the partial's store has completed
+      const unsigned int prev =
+          __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      is_last = (prev == static_cast<unsigned int>(split - 1));
+      if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      // Every arrival of this row has been counted: rest the counter at zero.
+      if (is_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    last = is_last;
+  }
+  __syncthreads();
+  if (!last) return;
+  const float t = fold_partials<Op, MEAN, true>(ws + r * split, split, cols);
+  if (threadIdx.x == 0) out[r] = t;
 }
 
-// Pass 2: one workgroup folds the `split` partials of a row in a fixed order
-// (lane-strided, then a wave64 butterfly, then the 4 waves in order).  Sums are
-// carried in double: the partials are few and this stage should not add error
-// on top of the first.
+// The fold as a launch of its own (one workgroup per row), for kTwoPass launches
+// that have no counter block.
 template <class Op, bool MEAN>
-__global__ __launch_bounds__(kThreads) void row_reduce_pass2_kernel(
+__global__ __launch_bounds__(kThreads) void row_reduce_fold_kernel(
     const float* __restrict__ ws, float* __restrict__ out, int64_t split, int64_t cols) {
   const int64_t r = blockIdx.x;
-  const float* p = ws + r * split;
-  const int w = threadIdx.x / kWave;
-  if constexpr (std::is_same_v<Op, SumOp>) {
-    __shared__ double part[kThreads / kWave];
-    double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < split; i += kThreads) acc += static_cast<double>(p[i]);
-#pragma unroll
-    for (int m = kWave / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
-    if ((threadIdx.x % kWave) == 0) part[w] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      double t = part[0];
-#pragma unroll
-      for (int i = 1; i < kThreads / kWave; ++i) t += part[i];
-      out[r] = static_cast<float>(MEAN ? t / static_cast<double>(cols) : t);
-    }
-  } else {
-    float acc = Op::identity();
-    for (int64_t i = threadIdx.x; i < split; i += kThreads) acc = Op::apply(acc, p[i]);
-    acc = block_combine_shfl<Op>(acc);
-    if (threadIdx.x == 0) out[r] = acc;
-  }
+  const float t = fold_partials<Op, MEAN, false>(ws + r * split, split, cols);
+  if (threadIdx.x == 0) out[r] = t;
+}
+
+// The counter block of `stream`, or -1 when the stream table is full.
+int counter_block(hipStream_t stream) {
+  static std::mutex mu;
+  static std::unordered_map<hipStream_t, int> blocks;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto it = blocks.find(stream);
+  if (it != blocks.end()) return it->second;
+  if (blocks.size() >= static_cast<std::size_t>(kCounterBlocks)) return -1;
+  const int b = static_cast<int>(blocks.size());
+  blocks.emplace(stream, b);
+  return b;
 }
 
 int64_t two_pass_split(int64_t rows, int64_t cols) {
@@ -217,15 +296,24 @@ int launch_two_pass(const float* x, float* out, int64_t rows, int64_t cols, floa
   int64_t chunk = (cols + split - 1) / split;
   chunk = (chunk + 3) & ~static_cast<int64_t>(3);
   const bool vec = (cols % 4 == 0) && aligned(x, 16);
+  int counter_base = -1;
+  if (split > 1 && rows <= kCountersPerBlock) {
+    const int b = counter_block(st);
+    if (b >= 0) counter_base = b * kCountersPerBlock;
+  }
   const dim3 g1(static_cast<unsigned>(split), static_cast<unsigned>(rows), 1u);
   if (vec)
-    row_reduce_pass1_kernel<Op, true><<<g1, kThreads, 0, st>>>(x, ws, cols, chunk, split);
+    row_reduce_split_kernel<Op, true, MEAN><<<g1, kThreads, 0, st>>>(x, ws, out, cols, chunk,
+                                                                     split, counter_base);
   else
-    row_reduce_pass1_kernel<Op, false><<<g1, kThreads, 0, st>>>(x, ws, cols, chunk, split);
-  MCKE_LAUNCH_CHECK("row_reduce_pass1_kernel");
-  row_reduce_pass2_kernel<Op, MEAN><<<static_cast<unsigned>(rows), kThreads, 0, st>>>(
-      ws, out, split, cols);
-  MCKE_LAUNCH_CHECK("row_reduce_pass2_kernel");
+    row_reduce_split_kernel<Op, false, MEAN><<<g1, kThreads, 0, st>>>(x, ws, out, cols, chunk,
+                                                                      split, counter_base);
+  MCKE_LAUNCH_CHECK("row_reduce_split_kernel");
+  if (split > 1 && counter_base < 0) {
+    row_reduce_fold_kernel<Op, MEAN><<<static_cast<unsigned>(rows), kThreads, 0, st>>>(
+        ws, out, split, cols);
+    MCKE_LAUNCH_CHECK("row_reduce_fold_kernel");
+  }
   return ok();
 }
 

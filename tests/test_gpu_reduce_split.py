@@ -1,0 +1,158 @@
+"""kTwoPass in one launch: the arrival counters behind the last-arrival fold.
+
+A kTwoPass launch whose rows are split over several workgroups counts the
+arrivals of each row on a counter that belongs to the launch's stream; the last
+workgroup of a row folds the row's partials and rests the counter at zero.  These
+tests check what that design has to guarantee, each against the double-
+accumulating CPU reduce (reference tests/reference.hpp:154-172; max bit-exact):
+
+* back-to-back launches of different shapes and kinds on one stream, with no
+  synchronisation between them, reuse the stream's counters correctly;
+* launches on several streams at once each count on their own counters;
+* once the stream table is full (a fresh process that has launched on 1024
+  streams), a launch on a further stream falls back to two launches and still
+  gives the same result.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+# (rows, cols, kind): every shape splits its rows (cols >= 8192 with fewer than
+# 256 rows), except the last two, which cover split == 1 between split launches.
+_SHAPES = [(1, 1 << 20, 0), (3, 40000, 1), (200, 8192, 2), (1, 8192, 0), (2, 100003, 0),
+           (255, 8200, 1), (7, 65536, 2), (1, 1 << 18, 1), (300, 9000, 0), (1, 4096, 0)]
+
+
+def _check(orc, x, rows, cols, kind, got):
+    want = orc.row_reduce(x, rows, cols, kind)
+    if kind == 1:
+        assert np.array_equal(got, want), f"max rows={rows} cols={cols}"
+        return
+    rms = float(np.sqrt(np.mean(np.square(x.astype(np.float64)))))
+    floor = 5e-5 * (rms / 0.577) * max(1.0, np.sqrt(cols / 4096.0))
+    if kind == 2:
+        floor /= cols
+    r = orc.compare(got, want, 1e-5, floor)
+    assert r.ok, f"kind={kind} rows={rows} cols={cols}: {r}"
+
+
+def _launch(m, dx, dout, rows, cols, kind, ws, wsb, stream=None):
+    m.launch_row_reduce_f32(dx, dout, rows, cols, kind, m.ReduceVariant.kTwoPass, ws, wsb,
+                            stream).throw_if_error()
+
+
+def test_back_to_back_on_one_stream(gpu, orc):
+    """Ten launches queued without a synchronisation; half share one workspace."""
+    m = gpu
+    D = m.DeviceBuffer
+    shared_wsb = max(m.row_reduce_workspace_bytes(r, c, m.ReduceVariant.kTwoPass)
+                     for r, c, _ in _SHAPES)
+    shared_ws = D(shared_wsb)
+    keep = []
+    for i, (rows, cols, kind) in enumerate(_SHAPES):
+        x = orc.fill_normal(rows * cols, 0x5EED12345 + i)
+        dx, dout = D.from_array(x), D(rows * 4)
+        if i % 2:
+            ws, wsb = shared_ws, shared_wsb
+        else:
+            wsb = max(m.row_reduce_workspace_bytes(rows, cols, m.ReduceVariant.kTwoPass), 4)
+            ws = D(wsb)
+        _launch(m, dx, dout, rows, cols, kind, ws, wsb)
+        keep.append((x, rows, cols, kind, dx, dout, ws))
+    m.device_synchronize()
+    for x, rows, cols, kind, _dx, dout, _ws in keep:
+        _check(orc, x, rows, cols, kind, dout.download(rows))
+
+
+def test_repeated_full_sum_same_bits(gpu, orc):
+    """The same full sum 20 times in a row on one stream: identical bits each time
+    (the fold's order is fixed) and equal to the CPU sum."""
+    m = gpu
+    D = m.DeviceBuffer
+    n = 1 << 24
+    x = orc.fill_random(n, 0xF011, 0.0, 1.0)
+    dx = D.from_array(x)
+    wsb = m.row_reduce_workspace_bytes(1, n, m.ReduceVariant.kTwoPass)
+    ws = D(wsb)
+    outs = [D(4) for _ in range(20)]
+    for o in outs:
+        _launch(m, dx, o, 1, n, 0, ws, wsb)
+    m.device_synchronize()
+    got = np.array([o.download(1)[0] for o in outs], np.float32)
+    assert np.all(got.view(np.uint32) == got.view(np.uint32)[0])
+    _check(orc, x, 1, n, 0, got[:1])
+
+
+def test_concurrent_streams(gpu, orc):
+    """Four streams, each with its own workspace, launching interleaved."""
+    m = gpu
+    D = m.DeviceBuffer
+    streams = [m.Stream() for _ in range(4)]
+    try:
+        work = []
+        for i in range(12):
+            rows, cols, kind = _SHAPES[i % 8]
+            x = orc.fill_normal(rows * cols, 0xC0C0 + i)
+            wsb = max(m.row_reduce_workspace_bytes(rows, cols, m.ReduceVariant.kTwoPass), 4)
+            dx, dout, ws = D.from_array(x), D(rows * 4), D(wsb)
+            work.append((x, rows, cols, kind, dx, dout, ws, wsb, streams[i % 4]))
+        for x, rows, cols, kind, dx, dout, ws, wsb, st in work:
+            _launch(m, dx, dout, rows, cols, kind, ws, wsb, st)
+        for st in streams:
+            st.synchronize()
+        for x, rows, cols, kind, _dx, dout, _ws, _wsb, _st in work:
+            _check(orc, x, rows, cols, kind, dout.download(rows))
+    finally:
+        for st in streams:
+            st.close()
+
+
+_FALLBACK_SCRIPT = r"""
+import sys
+sys.path.insert(0, {root!r})
+import numpy as np
+from __graft_entry__ import load_package
+import oracle
+m = load_package()
+m.require_gpu()
+D = m.DeviceBuffer
+TP = m.ReduceVariant.kTwoPass
+cols = 8192                      # rows == 1 splits in two
+x = oracle.fill_normal(cols, 0xFA11)
+dx = D.from_array(x)
+wsb = m.row_reduce_workspace_bytes(1, cols, TP)
+ws = D(wsb)
+streams, outs = [], []
+for i in range(1025):            # 1024 streams fill the table; the last one falls back
+    st = m.Stream()
+    o = D(4)
+    m.launch_row_reduce_f32(dx, o, 1, cols, 0, TP, ws if i == 0 else D(wsb), wsb, st).throw_if_error()
+    streams.append(st)
+    outs.append(o)
+m.device_synchronize()
+want = oracle.row_reduce(x, 1, cols, 0)
+got = np.array([o.download(1)[0] for o in outs], np.float32)
+bad = [i for i in range(len(got)) if got[i].view(np.uint32) != got[0].view(np.uint32)]
+assert not bad, f"streams {{bad[:5]}} differ: {{got[bad[:5]]}} vs {{got[0]}}"
+r = oracle.compare(got[:1], want, 1e-5, 5e-5 * 2.0)
+assert r.ok, str(r)
+print("fallback-ok", len(got))
+"""
+
+
+def test_stream_table_full_falls_back(gpu):
+    """In a fresh process: the 1025th stream takes the two-launch path and agrees
+    bit for bit with the counted one-launch path."""
+    code = _FALLBACK_SCRIPT.format(root=ROOT)
+    p = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    assert "fallback-ok 1025" in p.stdout
