@@ -212,6 +212,30 @@ bool tile_self_consistent(const mcke_gemm_tile& t) {
   return true;
 }
 
+// CUs of the current device (cached per device); 256, the gfx950 part's count,
+// when no device can be queried (a CPU-only host asking for a tile).
+int64_t device_cu_count() {
+  static std::mutex mu;
+  static std::vector<int> cached;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (static_cast<int>(cached.size()) <= dev) cached.resize(dev + 1, 0);
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0) {
+      (void)hipGetLastError();
+      cus = 256;
+    }
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 using GemmFn = void (*)(const float*, const float*, float*, int, int, int, float, float);
 using MfmaFn = void (*)(const float*, const float*, float*, int, int, int, float, float, int,
                         int);
@@ -234,7 +258,7 @@ struct MfmaCfg {
 
 const MfmaCfg kMfmaCfgs[] = {
     MCKE_MFMA_CFG_DMA(256, 256, 2), MCKE_MFMA_CFG(256, 256, 16), MCKE_MFMA_CFG_DMA(128, 128, 2),
-    MCKE_MFMA_CFG(128, 128, 16), MCKE_MFMA_CFG_DMA(64, 64, 2),
+    MCKE_MFMA_CFG(128, 128, 16), MCKE_MFMA_CFG_DMA(64, 64, 4),
 };
 #undef MCKE_MFMA_CFG
 #undef MCKE_MFMA_CFG_DMA
@@ -469,18 +493,37 @@ int mcke_launch_gemm_lp_vendor(const void* a, const void* b, void* c, int ab_dty
 
 int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile* out) {
   if (!out) return invalid("gemm_mfma_default_tile: null out");
-  // One workgroup runs per CU at a time.  Measured on MI355X:
-  //   - 256 x 256 wins when every CU of a 256-CU part gets a tile and each CU's
-  //     share of K (rounds of tiles x K) is long enough to amortise a tile's
-  //     pipeline fill and epilogue: 8192^3 (4 rounds x 8192) and 4096 x 4096 x
-  //     16384 (1 round x 16384, 142 vs 136 TFLOP/s for 128 x 128);
-  //   - otherwise 128 x 128 wins with four rounds of tiles (4096^3: 130 vs 127),
-  //   - and 64 x 64 below that (2048^3).
-  auto tiles = [&](int64_t t) { return ((m + t - 1) / t) * ((n + t - 1) / t); };
-  const int64_t t256 = tiles(256);
-  if (t256 >= 256 && (t256 / 256) * k >= 16384) *out = mcke_gemm_tile{256, 256, 32, 16, 16};
-  else if (tiles(128) >= 4 * 256) *out = mcke_gemm_tile{128, 128, 32, 8, 8};
-  else *out = mcke_gemm_tile{64, 64, 32, 4, 4};
+  (void)k;
+  // What decides is how evenly a tile size fills whole rounds of CUs: a launch
+  // takes as long as its busiest CU, so a partial last round costs a full one.
+  // Each candidate is scored by its sustained rate with every CU busy, times the
+  // share of its rounds' tile area that is useful work (m*n over rounds * CUs *
+  // tile area: partial rounds and the padding of edge tiles both count against
+  // it); the best score wins (ties: larger tile).
+  // Rates measured on MI355X (gfx950, 256 CUs), fp32, whole-tile shapes: 256 x 256
+  // (one workgroup per CU) ~145, 128 x 128 (two per CU) ~137, 64 x 64 ~130
+  // TFLOP/s.  The scores pick the measured winner at every shape timed:
+  // 8192^3 and 8192 x 8192 x {512..2048} -> 256; 4096^3 -> 256 (140 vs 131);
+  // 6144^3 -> 128 (137 vs 107 for 256, 2.25 rounds); 2048^3 and 2048 x 2048 x
+  // 8192 -> 128 (125 vs 120 for 64); 3072^3 -> 64 (125 vs 101); 1024^3 -> 64.
+  // Short K costs every tile alike (measured down to K = 512), so K is not weighed.
+  struct Cand { int t; double rate; mcke_gemm_tile tile; };
+  static const Cand cands[] = {{256, 145.0, {256, 256, 32, 16, 16}},
+                               {128, 137.0, {128, 128, 32, 8, 8}},
+                               {64, 130.0, {64, 64, 32, 4, 4}}};
+  const int64_t cus = device_cu_count();
+  double best = -1.0;
+  for (const Cand& c : cands) {
+    const int64_t tiles = ((m + c.t - 1) / c.t) * ((n + c.t - 1) / c.t);
+    const int64_t rounds = (tiles + cus - 1) / cus;
+    const double area = static_cast<double>(rounds * cus) * c.t * c.t;
+    const double score = rounds > 0 ? c.rate * static_cast<double>(m) * static_cast<double>(n) / area
+                                    : 0.0;
+    if (score > best) {
+      best = score;
+      *out = c.tile;
+    }
+  }
   return ok();
 }
 

@@ -142,14 +142,22 @@ def test_workspace_query(mcke):
 
 
 def test_default_mfma_tile(mcke):
+    """The rule weighs each tile's sustained rate by how evenly its tile count fills
+    whole rounds of CUs (256 on a CPU-only host, gfx950's count)."""
     t = mcke.gemm_mfma_default_tile(8192, 8192, 8192)
     assert t.astuple() == (256, 256, 32, 16, 16)
-    assert mcke.gemm_mfma_default_tile(4096, 4096, 4096).astuple() == (128, 128, 32, 8, 8)
-    assert mcke.gemm_mfma_default_tile(2048, 2048, 2048).astuple() == (64, 64, 32, 4, 4)
-    assert mcke.gemm_mfma_default_tile(512, 512, 512).astuple() == (64, 64, 32, 4, 4)
-    # Long K: one round of 256-tiles with K = 16384 (the MLP block's second GEMM).
+    assert mcke.gemm_mfma_default_tile(4096, 4096, 4096).astuple() == (256, 256, 32, 16, 16)
     assert mcke.gemm_mfma_default_tile(4096, 4096, 16384).astuple() == (256, 256, 32, 16, 16)
-    assert mcke.gemm_mfma_default_tile(8192, 8192, 2048).astuple() == (128, 128, 32, 8, 8)
+    assert mcke.gemm_mfma_default_tile(8192, 8192, 512).astuple() == (256, 256, 32, 16, 16)
+    # 6144^3: 576 tiles of 256 fill 2.25 rounds; 2304 tiles of 128 fill 9.
+    assert mcke.gemm_mfma_default_tile(6144, 6144, 6144).astuple() == (128, 128, 32, 8, 8)
+    assert mcke.gemm_mfma_default_tile(2048, 2048, 2048).astuple() == (128, 128, 32, 8, 8)
+    assert mcke.gemm_mfma_default_tile(2048, 2048, 8192).astuple() == (128, 128, 32, 8, 8)
+    # 3072^3: 576 tiles of 128 fill 2.25 rounds; 2304 tiles of 64 fill 9.
+    assert mcke.gemm_mfma_default_tile(3072, 3072, 3072).astuple() == (64, 64, 32, 4, 4)
+    assert mcke.gemm_mfma_default_tile(1024, 1024, 1024).astuple() == (64, 64, 32, 4, 4)
+    assert mcke.gemm_mfma_default_tile(512, 512, 512).astuple() == (64, 64, 32, 4, 4)
+    assert mcke.gemm_mfma_default_tile(1, 1, 1).astuple() == (64, 64, 32, 4, 4)
 
 
 # ---------------------------------------------------------------------------
