@@ -246,19 +246,28 @@ using MfmaFn = void (*)(const float*, const float*, float*, int, int, int, float
 struct MfmaCfg {
   int bm, bn, bk;
   MfmaFn even, vec, scalar;
+  int even_threads;   // block size of `even` (the staged kernels use 256)
 };
 
 #define MCKE_MFMA_CFG(BM, BN, BK)                                                     \
   {BM, BN, BK, &gemm_mfma_kernel<BM, BN, BK, true, true>,                            \
-   &gemm_mfma_kernel<BM, BN, BK, true, false>, &gemm_mfma_kernel<BM, BN, BK, false, false>}
-// BK = 32 whole tiles take the direct-to-LDS kernel.
-#define MCKE_MFMA_CFG_DMA(BM, BN, ST)                                                 \
-  {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST>, &gemm_mfma_kernel<BM, BN, 32, true, false>, \
-   &gemm_mfma_kernel<BM, BN, 32, false, false>}
+   &gemm_mfma_kernel<BM, BN, BK, true, false>, &gemm_mfma_kernel<BM, BN, BK, false, false>, \
+   kMfmaThreads}
+// BK = 32 whole tiles take the direct-to-LDS kernel (ST stages, KS wave groups
+// splitting each stage's K range).
+#define MCKE_MFMA_CFG_DMA(BM, BN, ST, KS)                                             \
+  {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST, KS>,                                \
+   &gemm_mfma_kernel<BM, BN, 32, true, false>, &gemm_mfma_kernel<BM, BN, 32, false, false>, \
+   kMfmaThreads * KS}
 
+// 64 x 64 tiles serve small problems, whose single round of tiles would leave
+// one wave per SIMD; two wave groups per tile measured 102.8 vs 89.9 TFLOP/s at
+// 1024^3 and 122.9 vs 120.4 at 2048^3.  For 128 x 128 they bought nothing
+// (124.9 vs 124.7 at 2048^3, 130.6 vs 134.3 at 4096^3).
 const MfmaCfg kMfmaCfgs[] = {
-    MCKE_MFMA_CFG_DMA(256, 256, 2), MCKE_MFMA_CFG(256, 256, 16), MCKE_MFMA_CFG_DMA(128, 128, 2),
-    MCKE_MFMA_CFG(128, 128, 16), MCKE_MFMA_CFG_DMA(64, 64, 4),
+    MCKE_MFMA_CFG_DMA(256, 256, 2, 1), MCKE_MFMA_CFG(256, 256, 16),
+    MCKE_MFMA_CFG_DMA(128, 128, 2, 1), MCKE_MFMA_CFG(128, 128, 16),
+    MCKE_MFMA_CFG_DMA(64, 64, 4, 2),
 };
 #undef MCKE_MFMA_CFG
 #undef MCKE_MFMA_CFG_DMA
@@ -274,8 +283,9 @@ struct Spec {
   GemmFn fn = nullptr;
   MfmaFn mfma = nullptr;
   MfmaFn mfma_even = nullptr;     // unchecked 16-byte variant for whole tiles
+  int even_threads = 0;           // its block size
   dim3 block{1, 1, 1};
-  int threads = 0;
+  int threads = 0;                // block size of `kernel`
   int tile_m = 0, tile_n = 0, tile_k = 0;
 };
 
@@ -333,9 +343,10 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
                        "(64,64,32,4,4); no fallback is applied");
       s.mfma = vec4 ? cfg->vec : cfg->scalar;
       s.mfma_even = vec4 ? cfg->even : nullptr;
+      s.even_threads = cfg->even_threads;
       s.tile_k = cfg->bk;
       s.block = dim3(kMfmaThreads, 1, 1);
-      s.threads = kMfmaThreads;
+      s.threads = s.mfma_even ? cfg->even_threads : kMfmaThreads;
       s.tile_m = cfg->bm;
       s.tile_n = cfg->bn;
       break;
@@ -425,7 +436,8 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
     const bool whole = sp.mfma_even && m % sp.tile_m == 0 && n % sp.tile_n == 0 &&
                        k % sp.tile_k == 0;
     const MfmaFn fn = whole ? sp.mfma_even : sp.mfma;
-    fn<<<static_cast<unsigned>(tiles_m * tiles_n), sp.block, 0, s>>>(
+    const dim3 block = whole ? dim3(static_cast<unsigned>(sp.even_threads), 1, 1) : sp.block;
+    fn<<<static_cast<unsigned>(tiles_m * tiles_n), block, 0, s>>>(
         a, b, c, mi, ni, ki, alpha, beta, static_cast<int>(tiles_m), static_cast<int>(tiles_n));
     MCKE_LAUNCH_CHECK("gemm_mfma_kernel");
     return ok();
@@ -501,8 +513,8 @@ int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile*
   // tile area: partial rounds and the padding of edge tiles both count against
   // it); the best score wins (ties: larger tile).
   // Rates measured on MI355X (gfx950, 256 CUs), fp32, whole-tile shapes: 256 x 256
-  // (one workgroup per CU) ~145, 128 x 128 (two per CU) ~137, 64 x 64 ~130
-  // TFLOP/s.  The scores pick the measured winner at every shape timed:
+  // (one workgroup per CU) ~145, 128 x 128 (two per CU) ~137, 64 x 64 (two wave
+  // groups per tile) ~128 TFLOP/s.  The scores pick the measured winner at every shape timed:
   // 8192^3 and 8192 x 8192 x {512..2048} -> 256; 4096^3 -> 256 (140 vs 131);
   // 6144^3 -> 128 (137 vs 107 for 256, 2.25 rounds); 2048^3 and 2048 x 2048 x
   // 8192 -> 128 (125 vs 120 for 64); 3072^3 -> 64 (125 vs 101); 1024^3 -> 64.
@@ -510,7 +522,7 @@ int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile*
   struct Cand { int t; double rate; mcke_gemm_tile tile; };
   static const Cand cands[] = {{256, 145.0, {256, 256, 32, 16, 16}},
                                {128, 137.0, {128, 128, 32, 8, 8}},
-                               {64, 130.0, {64, 64, 32, 4, 4}}};
+                               {64, 128.0, {64, 64, 32, 4, 4}}};
   const int64_t cus = device_cu_count();
   double best = -1.0;
   for (const Cand& c : cands) {

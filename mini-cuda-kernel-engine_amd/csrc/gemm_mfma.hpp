@@ -417,23 +417,39 @@ __device__ __forceinline__ void mfma_dma_issue(int i, int na, int nb, int a_floa
   }
 }
 
-template <int BM, int BN, int STAGES>
-__global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
+// KS > 1 splits each stage's K range over KS groups of 4 waves (4 KS waves per
+// workgroup): group g runs the MFMA sub-steps of k-quarters [g Q/KS, (g+1) Q/KS)
+// of every stage into accumulators of its own, all groups read the same LDS
+// stages, and at the end groups 1 .. KS-1 hand their accumulators to group 0
+// through LDS, which adds them in group order and writes C.  It puts KS waves on
+// each SIMD for the same tile, so one wave's LDS waits and barrier skew hide
+// under another's MFMAs -- the case of small problems, whose one round of tiles
+// leaves one wave per SIMD.  The sum order over K differs from KS = 1 (the
+// groups' partials are added last), and is fixed for a given KS.
+template <int BM, int BN, int STAGES, int KS = 1>
+__global__ __launch_bounds__(kMfmaThreads * KS, 1) void gemm_mfma_dma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
   constexpr int BK = 32;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int MT = WM / 32, NT = WN / 32;
   static_assert(MT >= 1 && (NT == 1 || NT == 2 || NT == 4), "unsupported wave tile");
+  constexpr int kWaves = 4 * KS;
   constexpr int kAFloats = BM * BK;
   constexpr int kStageFloats = kAFloats + BK * BN;
   constexpr int kAChunks = kAFloats / 256, kBChunks = BK * BN / 256;   // 1 KB chunks
-  constexpr int NA = kAChunks / 4, NB = kBChunks / 4;                   // per wave
-  static_assert(kAChunks % 4 == 0 && kBChunks % 4 == 0, "chunks must split over 4 waves");
+  constexpr int NA = kAChunks / kWaves, NB = kBChunks / kWaves;         // per wave
+  static_assert(kAChunks % kWaves == 0 && kBChunks % kWaves == 0,
+                "chunks must split over the workgroup's waves");
   constexpr int L = NA + NB;            // DMA instructions per wave per stage
-  constexpr int P = BK / 2;             // MFMA sub-steps per stage
+  constexpr int Q = BK / 8;             // k-quarters per stage (4 MFMA sub-steps each)
+  static_assert(Q % KS == 0, "the k-quarters must split over the wave groups");
+  constexpr int QG = Q / KS;            // k-quarters per wave group
+  constexpr int P = 4 * QG;             // MFMA sub-steps per wave per stage
   using BV = typename BVec<NT>::type;
   static_assert(STAGES >= 2 && (STAGES - 2) * L <= 63, "vmcnt counts at most 63 loads");
+  static_assert(KS == 1 || (KS - 1) * 4 * MT * NT * 16 * kWave <= STAGES * kStageFloats,
+                "the groups' accumulators must fit in the stage buffers");
 
   __shared__ __attribute__((aligned(16))) float smem[STAGES * kStageFloats];
 
@@ -443,7 +459,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  const int wm = wave / 2, wn = wave % 2;
+  const int kg = wave / 4;              // wave group (K split)
+  const int w4 = wave % 4;
+  const int wm = w4 / 2, wn = w4 % 2;
   const int h = lane / 32, c = lane % 32;
 
   // This lane's source addresses for its wave's chunks of stage 0 (advanced by BK
@@ -488,13 +506,14 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
   }
 
   // Fragment addressing: rows wm*WM + i*32 + c all share f = f(c) (the row base
-  // is a multiple of 16); k-slot 4h + q sits at position (4h + q) ^ f.
+  // is a multiple of 16); k-slot 4h + q sits at position (4h + q) ^ f.  This
+  // wave's group walks k-quarters q = kg*QG + qq, qq < QG.
   const int f = (c & 7) ^ ((c >> 3) & 1);
   const int a_row = (wm * WM + c) * BK;
-  int a_q[BK / 8];
+  int a_q[QG];
 #pragma unroll
-  for (int q = 0; q < BK / 8; ++q) a_q[q] = 4 * ((4 * h + q) ^ f);
-  const int b_off = kAFloats + (h * (BK / 2)) * BN + wn * WN + NT * c;
+  for (int qq = 0; qq < QG; ++qq) a_q[qq] = 4 * ((4 * h + kg * QG + qq) ^ f);
+  const int b_off = kAFloats + (h * (BK / 2) + 4 * kg * QG) * BN + wn * WN + NT * c;
 
   for (int ks = 0; ks < ksteps; ++ks) {
     // Stage ks has landed once at most the (STAGES - 2) younger stages' loads are
@@ -520,19 +539,19 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
       av[i] = *reinterpret_cast<const f32x4*>(stage + a_row + i * 32 * BK + a_q[0]);
     BV bv = *reinterpret_cast<const BV*>(stage + b_off);
 #pragma unroll
-    for (int q = 0; q < BK / 8; ++q) {
+    for (int qq = 0; qq < QG; ++qq) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int p = 4 * q + s;
+        const int p = 4 * qq + s;
         BV bv_next = bv;
         if (s < 3) {
-          bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + s + 1) * BN);
-        } else if (q + 1 < BK / 8) {
-          bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + 4) * BN);
+          bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * qq + s + 1) * BN);
+        } else if (qq + 1 < QG) {
+          bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * qq + 4) * BN);
 #pragma unroll
           for (int i = 0; i < MT; ++i)
             av_next[i] =
-                *reinterpret_cast<const f32x4*>(stage + a_row + i * 32 * BK + a_q[q + 1]);
+                *reinterpret_cast<const f32x4*>(stage + a_row + i * 32 * BK + a_q[qq + 1]);
         }
         // The fetch of stage ks + STAGES - 1, spread over the first half of the
         // sub-steps so that its issue hides under the MFMAs.
@@ -552,15 +571,43 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_dma_kernel(
         }
         __builtin_amdgcn_sched_barrier(0);
         bv = bv_next;
-        if (s == 3 && q + 1 < BK / 8) {
+        if (s == 3 && qq + 1 < QG) {
 #pragma unroll
           for (int i = 0; i < MT; ++i) av[i] = av_next[i];
         }
       }
     }
   }
-  // No LDS DMA may still be landing when the workgroup retires.
+  // No LDS DMA may still be landing when the workgroup retires (or, with KS > 1,
+  // when the stage buffers are reused below).
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  if constexpr (KS > 1) {
+    // Groups 1 .. KS-1 park their accumulators in the (now idle) stage buffers,
+    // lane-contiguous per register; group 0 adds them in group order.
+    __syncthreads();
+    auto slot = [&](int g, int i, int j, int r) {
+      return ((((g - 1) * 4 + w4) * MT + i) * NT + j) * 16 * kWave + r * kWave + lane;
+    };
+    if (kg > 0) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) smem[slot(kg, i, j, r)] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int g = 1; g < KS; ++g)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += smem[slot(g, i, j, r)];
+  }
 
   mfma_store_c<BM, BN, true>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
 }

@@ -259,3 +259,39 @@ def test_gemm_512_baseline_config(gpu, orc):
     assert r.ok, str(r)
     r2 = orc.compare(got, want, orc.tol_gemm(n), orc.abs_tol_gemm(n))
     assert r2.ok, str(r2)
+
+
+def test_mfma_kernel_attrs_report_the_whole_tile_kernel(gpu):
+    """gemm_kernel_attrs (kernels.hpp:293-302) describes the kernel that whole-tile
+    shapes run: the 64x64 tile's direct-to-LDS kernel runs two wave groups (512
+    lanes), the larger tiles one (256 lanes)."""
+    T = gpu.GemmTile
+    for tile, threads in ((T(64, 64, 32, 4, 4), 512), (T(128, 128, 32, 8, 8), 256),
+                          (T(256, 256, 32, 16, 16), 256)):
+        st, at = gpu.gemm_kernel_attrs(gpu.GemmVariant.kMfmaF32, tile)
+        assert st.ok(), str(st)
+        assert at.threads_per_block == threads, tile.astuple()
+        assert at.max_blocks_per_sm_api >= 1 and at.local_bytes == 0, tile.astuple()
+
+
+@pytest.mark.parametrize("n", [64, 192, 512, 1024])
+def test_gemm_64_tile_two_wave_groups(gpu, orc, n):
+    """The 64x64 whole-tile kernel folds its two wave groups' K halves in a fixed
+    order: the full reference (reference.hpp:199-211) at the K-scaled tolerance,
+    the same bits on a second launch, and beta = 0 never reading a NaN-poisoned C."""
+    a = orc.fill_random(n * n, 0x6E33A + n)
+    b = orc.fill_random(n * n, 0x8B10C + n)
+    t = gpu.GemmTile(64, 64, 32, 4, 4)
+    want = orc.gemm(a, b, np.zeros(n * n, np.float32), n, n, n)
+    poisoned = np.full(n * n, np.nan, np.float32)
+    got = run_gemm(gpu, a, b, poisoned, n, n, n, 1.0, 0.0, gpu.GemmVariant.kMfmaF32, t)
+    r = orc.compare(got, want, orc.tol_gemm(n), orc.abs_tol_gemm(n))
+    assert r.ok, str(r)
+    again = run_gemm(gpu, a, b, poisoned, n, n, n, 1.0, 0.0, gpu.GemmVariant.kMfmaF32, t)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    # alpha / beta epilogue on the same kernel
+    c0 = orc.fill_random(n * n, 0xC0FFEE)
+    got = run_gemm(gpu, a, b, c0, n, n, n, 0.5, 2.0, gpu.GemmVariant.kMfmaF32, t)
+    want = orc.gemm(a, b, c0, n, n, n, 0.5, 2.0)
+    r = orc.compare(got, want, orc.tol_gemm(n), orc.abs_tol_gemm(n) * 2.0)
+    assert r.ok, str(r)
