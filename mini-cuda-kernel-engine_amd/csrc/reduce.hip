@@ -27,8 +27,10 @@
 #include <cmath>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <type_traits>
 #include <unordered_map>
+#include <utility>
 
 #include "common.hpp"
 #include "device_math.hpp"
@@ -51,7 +53,8 @@ constexpr int64_t kMaxSplit = 65535;
 
 // Arrival counters of kTwoPass rows, owned by the library (zero when the code
 // object loads).  A launch takes the block of kCountersPerBlock counters that
-// belongs to its stream, one counter per row.  Launches on one stream run one
+// belongs to its stream (for the per-thread default stream: to that stream in
+// the calling thread), one counter per row.  Launches on one stream run one
 // after another -- and a captured graph keeps the order of the nodes captured
 // on one stream -- so two launches that run at the same time never share a
 // counter.  Every counter is zero at rest: the workgroup that arrives last on a
@@ -249,16 +252,27 @@ __global__ __launch_bounds__(kThreads) void row_reduce_fold_kernel(
   if (threadIdx.x == 0) out[r] = t;
 }
 
-// The counter block of `stream`, or -1 when the stream table is full.
+// The counter block of `stream`, or -1 when the stream table is full.  The
+// per-thread default stream is one handle value that names a different stream
+// in each host thread, so it is keyed by the calling thread as well; every
+// other handle (the legacy null stream included) names one stream whatever
+// thread launches on it.
 int counter_block(hipStream_t stream) {
+  using Key = std::pair<hipStream_t, std::thread::id>;
+  struct KeyHash {
+    std::size_t operator()(const Key& k) const {
+      return std::hash<const void*>()(k.first) ^ (std::hash<std::thread::id>()(k.second) << 1);
+    }
+  };
   static std::mutex mu;
-  static std::unordered_map<hipStream_t, int> blocks;
+  static std::unordered_map<Key, int, KeyHash> blocks;
+  const Key key{stream, stream == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id()};
   std::lock_guard<std::mutex> lock(mu);
-  const auto it = blocks.find(stream);
+  const auto it = blocks.find(key);
   if (it != blocks.end()) return it->second;
   if (blocks.size() >= static_cast<std::size_t>(kCounterBlocks)) return -1;
   const int b = static_cast<int>(blocks.size());
-  blocks.emplace(stream, b);
+  blocks.emplace(key, b);
   return b;
 }
 

@@ -8,7 +8,8 @@ accumulating CPU reduce (reference tests/reference.hpp:154-172; max bit-exact):
 
 * back-to-back launches of different shapes and kinds on one stream, with no
   synchronisation between them, reuse the stream's counters correctly;
-* launches on several streams at once each count on their own counters;
+* launches on several streams at once each count on their own counters, and so
+  do two host threads launching on the per-thread default stream;
 * once the stream table is full (a fresh process that has launched on 1024
   streams), a launch on a further stream falls back to two launches and still
   gives the same result.
@@ -156,3 +157,40 @@ def test_stream_table_full_falls_back(gpu):
     p = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
     assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
     assert "fallback-ok 1025" in p.stdout
+
+
+def test_per_thread_default_stream_in_two_threads(gpu, orc):
+    """hipStreamPerThread is one handle naming a different stream in each host
+    thread: two threads launching on it at once each get counters of their own
+    (the launches are ctypes calls, which release the GIL, so they interleave)."""
+    import threading
+
+    m = gpu
+    D = m.DeviceBuffer
+    per_thread = 2                       # hipStreamPerThread
+    n = 1 << 20
+    inputs = [orc.fill_random(n, 0x7EAD + t, 0.0, 1.0) for t in range(2)]
+    wsb = m.row_reduce_workspace_bytes(1, n, m.ReduceVariant.kTwoPass)
+    dev = [(D.from_array(x), D(wsb), [D(4) for _ in range(16)]) for x in inputs]
+    errors = []
+
+    def worker(t):
+        try:
+            dx, ws, outs = dev[t]
+            for o in outs:
+                _launch(m, dx, o, 1, n, 0, ws, wsb, per_thread)
+            assert m.lib().mcke_rt_stream_synchronize(per_thread) == 0
+        except Exception as e:          # reported after join
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    m.device_synchronize()
+    for t, (_dx, _ws, outs) in enumerate(dev):
+        got = np.array([o.download(1)[0] for o in outs], np.float32)
+        _check(orc, inputs[t], 1, n, 0, got[:1])
+        assert np.all(got.view(np.uint32) == got.view(np.uint32)[0]), f"thread {t}"
