@@ -584,4 +584,5 @@ MFMA_TILES = (
     GemmTile(128, 128, 32, 8, 8),
     GemmTile(128, 128, 16, 8, 8),
     GemmTile(64, 64, 32, 4, 4),
+    GemmTile(32, 32, 32, 2, 2),
 )

@@ -258,16 +258,18 @@ struct MfmaCfg {
 #define MCKE_MFMA_CFG_DMA(BM, BN, ST, KS)                                             \
   {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST, KS>,                                \
    &gemm_mfma_kernel<BM, BN, 32, true, false>, &gemm_mfma_kernel<BM, BN, 32, false, false>, \
-   kMfmaThreads * KS}
+   kDmaThreads<BM, BN, KS>}
 
 // 64 x 64 tiles serve small problems, whose single round of tiles would leave
 // one wave per SIMD; two wave groups per tile measured 102.8 vs 89.9 TFLOP/s at
 // 1024^3 and 122.9 vs 120.4 at 2048^3.  For 128 x 128 they bought nothing
-// (124.9 vs 124.7 at 2048^3, 130.6 vs 134.3 at 4096^3).
+// (124.9 vs 124.7 at 2048^3, 130.6 vs 134.3 at 4096^3).  32 x 32 tiles (one wave
+// wide, four groups) give the smallest problems four times the workgroups of
+// 64 x 64: 40.0 vs 22.6 TFLOP/s at 512^3, 7.0 vs 4.5 at 256^3.
 const MfmaCfg kMfmaCfgs[] = {
     MCKE_MFMA_CFG_DMA(256, 256, 2, 1), MCKE_MFMA_CFG(256, 256, 16),
     MCKE_MFMA_CFG_DMA(128, 128, 2, 1), MCKE_MFMA_CFG(128, 128, 16),
-    MCKE_MFMA_CFG_DMA(64, 64, 4, 2),
+    MCKE_MFMA_CFG_DMA(64, 64, 4, 2),   MCKE_MFMA_CFG_DMA(32, 32, 4, 4),
 };
 #undef MCKE_MFMA_CFG
 #undef MCKE_MFMA_CFG_DMA
@@ -339,8 +341,8 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
       const MfmaCfg* cfg = find_mfma(*tile);
       if (!cfg)
         return invalid("launch_gemm_f32: kMfmaF32 is instantiated for tiles (256,256,32,16,16), "
-                       "(256,256,16,16,16), (128,128,32,8,8), (128,128,16,8,8) and "
-                       "(64,64,32,4,4); no fallback is applied");
+                       "(256,256,16,16,16), (128,128,32,8,8), (128,128,16,8,8), "
+                       "(64,64,32,4,4) and (32,32,32,2,2); no fallback is applied");
       s.mfma = vec4 ? cfg->vec : cfg->scalar;
       s.mfma_even = vec4 ? cfg->even : nullptr;
       s.even_threads = cfg->even_threads;
@@ -514,15 +516,17 @@ int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile*
   // it); the best score wins (ties: larger tile).
   // Rates measured on MI355X (gfx950, 256 CUs), fp32, whole-tile shapes: 256 x 256
   // (one workgroup per CU) ~145, 128 x 128 (two per CU) ~137, 64 x 64 (two wave
-  // groups per tile) ~128 TFLOP/s.  The scores pick the measured winner at every shape timed:
+  // groups per tile) ~128, 32 x 32 (four groups) ~100 TFLOP/s.  The scores pick the measured winner at every shape timed:
   // 8192^3 and 8192 x 8192 x {512..2048} -> 256; 4096^3 -> 256 (140 vs 131);
   // 6144^3 -> 128 (137 vs 107 for 256, 2.25 rounds); 2048^3 and 2048 x 2048 x
-  // 8192 -> 128 (125 vs 120 for 64); 3072^3 -> 64 (125 vs 101); 1024^3 -> 64.
+  // 8192 -> 128 (125 vs 120 for 64); 3072^3 -> 64 (125 vs 101); 1024^3 -> 64
+  // (103 vs 85 for 32); 512^3 -> 32 (40 vs 23 for 64); 256^3 -> 32.
   // Short K costs every tile alike (measured down to K = 512), so K is not weighed.
   struct Cand { int t; double rate; mcke_gemm_tile tile; };
   static const Cand cands[] = {{256, 145.0, {256, 256, 32, 16, 16}},
                                {128, 137.0, {128, 128, 32, 8, 8}},
-                               {64, 128.0, {64, 64, 32, 4, 4}}};
+                               {64, 128.0, {64, 64, 32, 4, 4}},
+                               {32, 100.0, {32, 32, 32, 2, 2}}};
   const int64_t cus = device_cu_count();
   double best = -1.0;
   for (const Cand& c : cands) {

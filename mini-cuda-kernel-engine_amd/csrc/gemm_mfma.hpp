@@ -170,17 +170,17 @@ struct MfmaStage {
   }
 };
 
-// Epilogue shared by the MFMA kernels: C = alpha * acc + beta * C for the
-// workgroup's BM x BN tile (C is not read when beta == 0).  Lane (h, c) of wave
-// (wm, wn) holds, for MFMA tile (i, j) and accumulator register r, row
+// Epilogue shared by the MFMA kernels: C = alpha * acc + beta * C for one wave's
+// MT x NT accumulator tiles, the WM x WN = 32 MT x 32 NT block at wave position
+// (wm, wn) of the workgroup's tile at (m0, n0) (C is not read when beta == 0).
+// Lane (h, c) holds, for MFMA tile (i, j) and accumulator register r, row
 // 8*(r/4) + 4h + r%4 of the tile's 32 rows and column NT*c + j of the wave's WN.
-template <int BM, int BN, bool VEC>
-__device__ __forceinline__ void mfma_store_c(const f32x16 (&acc)[BM / 64][BN / 64],
+template <int MT, int NT, bool VEC>
+__device__ __forceinline__ void mfma_store_c(const f32x16 (&acc)[MT][NT],
                                              float* __restrict__ C, int M, int N, int m0, int n0,
                                              int wm, int wn, int h, int c, float alpha,
                                              float beta) {
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int MT = WM / 32, NT = WN / 32;
+  constexpr int WM = 32 * MT, WN = 32 * NT;
   const bool vec_store = VEC && (NT == 4) && ((N & 3) == 0);
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
@@ -261,15 +261,36 @@ struct MfmaVecIO {
   }
 };
 
+// Waves of one group: a 2 x 2 grid over the tile for tiles of 64 and more, one
+// wave across a dimension of 32.  A kernel with more waves than one group runs
+// several groups, which split each stage's K range (see gemm_mfma_dma_kernel).
+template <int BM> constexpr int kMfmaWaveRows = BM >= 64 ? 2 : 1;
+template <int BN> constexpr int kMfmaWaveCols = BN >= 64 ? 2 : 1;
+template <int BM, int BN, int KS>
+constexpr int kDmaThreads = kWave * kMfmaWaveRows<BM> * kMfmaWaveCols<BN> * KS;
+
 template <int BM, int BN, int BK, bool VEC, bool EVEN>
 __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
-  constexpr int WM = BM / 2, WN = BN / 2;
+  // The 256 lanes form one 2 x 2 wave grid for tiles of 64 and more; a 32 x 32
+  // tile is one wave wide and high, and its 4 waves are 4 groups splitting each
+  // stage's K range, folded in group order at the end.
+  constexpr int WGM = kMfmaWaveRows<BM>, WGN = kMfmaWaveCols<BN>;
+  constexpr int WPG = WGM * WGN;
+  constexpr int KS = (kMfmaThreads / kWave) / WPG;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int MT = WM / 32, NT = WN / 32;
-  static_assert(MT >= 1 && (NT == 1 || NT == 2 || NT == 4), "unsupported wave tile");
+  static_assert(MT >= 1 && WM == 32 * MT && (NT == 1 || NT == 2 || NT == 4),
+                "unsupported wave tile");
+  static_assert(KS * WPG * kWave == kMfmaThreads, "the waves must form whole groups");
   static_assert(BK % 8 == 0, "BK must be a multiple of 8 (two halves of 4-deep reads)");
+  constexpr int Q = BK / 8;             // k-quarters per stage
+  static_assert(Q % KS == 0, "the k-quarters must split over the wave groups");
+  constexpr int QG = Q / KS;            // k-quarters per wave group
   using S = MfmaStage<BM, BN, BK, VEC>;
+  static_assert(KS == 1 || (KS - 1) * WPG * MT * NT * 16 * kWave <= 2 * S::kStageFloats,
+                "the groups' accumulators must fit in the stage buffers");
   using BV = typename BVec<NT>::type;
 
   __shared__ __attribute__((aligned(16))) float smem[2 * S::kStageFloats];
@@ -280,7 +301,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  const int wm = wave / 2, wn = wave % 2;
+  const int kg = wave / WPG;            // wave group (K split)
+  const int wg = wave % WPG;            // wave within its group
+  const int wm = wg / WGN, wn = wg % WGN;
   const int h = lane / 32, c = lane % 32;
 
   f32x16 acc[MT][NT];
@@ -299,9 +322,10 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
   }
   __syncthreads();
 
-  // Per-lane LDS offsets (floats) inside a stage.
-  const int a_off = (wm * WM + c) * S::kLdA + h * (BK / 2);
-  const int b_off = S::kAFloats + (h * (BK / 2)) * S::kLdB + wn * WN + NT * c;
+  // Per-lane LDS offsets (floats) inside a stage, at this wave group's first
+  // k-quarter.
+  const int a_off = (wm * WM + c) * S::kLdA + h * (BK / 2) + 4 * kg * QG;
+  const int b_off = S::kAFloats + (h * (BK / 2) + 4 * kg * QG) * S::kLdB + wn * WN + NT * c;
 
   // The next stage's global loads and LDS stores.  On the 16-byte path they are
   // spread over the MFMA stream of the current stage -- loads over the first half
@@ -309,7 +333,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
   // the previous barrier) over the second half -- so the matrix pipe never waits
   // for their issue.  The last stage re-loads itself (k0 clamped) and stores into
   // the unused buffer: harmless, and it keeps the loop free of branches.
-  constexpr int P = BK / 2;
+  constexpr int P = 4 * QG;              // MFMA sub-steps per wave per stage
   using IO = MfmaVecIO<BM, BN, BK>;
   constexpr int L = IO::kLoads;
 
@@ -331,14 +355,14 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
       av[i] = *reinterpret_cast<const f32x4*>(stage + a_off + i * 32 * S::kLdA);
     BV bv = *reinterpret_cast<const BV*>(stage + b_off);
 #pragma unroll
-    for (int q = 0; q < BK / 8; ++q) {
+    for (int q = 0; q < QG; ++q) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int p = 4 * q + s;
         BV bv_next = bv;
         if (s < 3) {
           bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + s + 1) * S::kLdB);
-        } else if (q + 1 < BK / 8) {
+        } else if (q + 1 < QG) {
           bv_next = *reinterpret_cast<const BV*>(stage + b_off + (4 * q + 4) * S::kLdB);
 #pragma unroll
           for (int i = 0; i < MT; ++i)
@@ -368,7 +392,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
             if (P / 2 + (i * (P / 2)) / L == p) IO::store_one(R, i, next_stage);
         }
         bv = bv_next;
-        if (s == 3 && q + 1 < BK / 8) {
+        if (s == 3 && q + 1 < QG) {
 #pragma unroll
           for (int i = 0; i < MT; ++i) av[i] = av_next[i];
         }
@@ -381,7 +405,34 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
     __syncthreads();
   }
 
-  mfma_store_c<BM, BN, VEC>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
+  if constexpr (KS > 1) {
+    // Groups 1 .. KS-1 park their accumulators in the stage buffers (free after
+    // the loop's last barrier), lane-contiguous per register; group 0 adds them in
+    // group order.
+    auto slot = [&](int g, int i, int j, int r) {
+      return ((((g - 1) * WPG + wg) * MT + i) * NT + j) * 16 * kWave + r * kWave + lane;
+    };
+    if (kg > 0) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) smem[slot(kg, i, j, r)] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int g = 1; g < KS; ++g)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += smem[slot(g, i, j, r)];
+  }
+
+  mfma_store_c<MT, NT, VEC>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
 }
 
 
@@ -417,8 +468,8 @@ __device__ __forceinline__ void mfma_dma_issue(int i, int na, int nb, int a_floa
   }
 }
 
-// KS > 1 splits each stage's K range over KS groups of 4 waves (4 KS waves per
-// workgroup): group g runs the MFMA sub-steps of k-quarters [g Q/KS, (g+1) Q/KS)
+// KS > 1 splits each stage's K range over KS groups of waves (each group a 2 x 2
+// grid, or 1 x 1 for a 32 x 32 tile): group g runs the MFMA sub-steps of k-quarters [g Q/KS, (g+1) Q/KS)
 // of every stage into accumulators of its own, all groups read the same LDS
 // stages, and at the end groups 1 .. KS-1 hand their accumulators to group 0
 // through LDS, which adds them in group order and writes C.  It puts KS waves on
@@ -427,14 +478,17 @@ __device__ __forceinline__ void mfma_dma_issue(int i, int na, int nb, int a_floa
 // leaves one wave per SIMD.  The sum order over K differs from KS = 1 (the
 // groups' partials are added last), and is fixed for a given KS.
 template <int BM, int BN, int STAGES, int KS = 1>
-__global__ __launch_bounds__(kMfmaThreads * KS, 1) void gemm_mfma_dma_kernel(
+__global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
     int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
   constexpr int BK = 32;
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WGM = kMfmaWaveRows<BM>, WGN = kMfmaWaveCols<BN>;
+  constexpr int WPG = WGM * WGN;        // waves per group
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int MT = WM / 32, NT = WN / 32;
-  static_assert(MT >= 1 && (NT == 1 || NT == 2 || NT == 4), "unsupported wave tile");
-  constexpr int kWaves = 4 * KS;
+  static_assert(MT >= 1 && WM == 32 * MT && (NT == 1 || NT == 2 || NT == 4),
+                "unsupported wave tile");
+  constexpr int kWaves = WPG * KS;
   constexpr int kAFloats = BM * BK;
   constexpr int kStageFloats = kAFloats + BK * BN;
   constexpr int kAChunks = kAFloats / 256, kBChunks = BK * BN / 256;   // 1 KB chunks
@@ -448,7 +502,7 @@ __global__ __launch_bounds__(kMfmaThreads * KS, 1) void gemm_mfma_dma_kernel(
   constexpr int P = 4 * QG;             // MFMA sub-steps per wave per stage
   using BV = typename BVec<NT>::type;
   static_assert(STAGES >= 2 && (STAGES - 2) * L <= 63, "vmcnt counts at most 63 loads");
-  static_assert(KS == 1 || (KS - 1) * 4 * MT * NT * 16 * kWave <= STAGES * kStageFloats,
+  static_assert(KS == 1 || (KS - 1) * WPG * MT * NT * 16 * kWave <= STAGES * kStageFloats,
                 "the groups' accumulators must fit in the stage buffers");
 
   __shared__ __attribute__((aligned(16))) float smem[STAGES * kStageFloats];
@@ -459,9 +513,9 @@ __global__ __launch_bounds__(kMfmaThreads * KS, 1) void gemm_mfma_dma_kernel(
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  const int kg = wave / 4;              // wave group (K split)
-  const int w4 = wave % 4;
-  const int wm = w4 / 2, wn = w4 % 2;
+  const int kg = wave / WPG;            // wave group (K split)
+  const int wg = wave % WPG;            // wave within its group
+  const int wm = wg / WGN, wn = wg % WGN;
   const int h = lane / 32, c = lane % 32;
 
   // This lane's source addresses for its wave's chunks of stage 0 (advanced by BK
@@ -587,7 +641,7 @@ __global__ __launch_bounds__(kMfmaThreads * KS, 1) void gemm_mfma_dma_kernel(
     // lane-contiguous per register; group 0 adds them in group order.
     __syncthreads();
     auto slot = [&](int g, int i, int j, int r) {
-      return ((((g - 1) * 4 + w4) * MT + i) * NT + j) * 16 * kWave + r * kWave + lane;
+      return ((((g - 1) * WPG + wg) * MT + i) * NT + j) * 16 * kWave + r * kWave + lane;
     };
     if (kg > 0) {
 #pragma unroll
@@ -609,7 +663,7 @@ __global__ __launch_bounds__(kMfmaThreads * KS, 1) void gemm_mfma_dma_kernel(
           for (int r = 0; r < 16; ++r) acc[i][j][r] += smem[slot(g, i, j, r)];
   }
 
-  mfma_store_c<BM, BN, true>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
+  mfma_store_c<MT, NT, true>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
 }
 
 }  // namespace mcke_amd

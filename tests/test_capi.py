@@ -156,8 +156,10 @@ def test_default_mfma_tile(mcke):
     # 3072^3: 576 tiles of 128 fill 2.25 rounds; 2304 tiles of 64 fill 9.
     assert mcke.gemm_mfma_default_tile(3072, 3072, 3072).astuple() == (64, 64, 32, 4, 4)
     assert mcke.gemm_mfma_default_tile(1024, 1024, 1024).astuple() == (64, 64, 32, 4, 4)
-    assert mcke.gemm_mfma_default_tile(512, 512, 512).astuple() == (64, 64, 32, 4, 4)
-    assert mcke.gemm_mfma_default_tile(1, 1, 1).astuple() == (64, 64, 32, 4, 4)
+    # 512^3: 64 tiles of 64 fill a quarter round; 256 tiles of 32 fill one.
+    assert mcke.gemm_mfma_default_tile(512, 512, 512).astuple() == (32, 32, 32, 2, 2)
+    assert mcke.gemm_mfma_default_tile(256, 256, 256).astuple() == (32, 32, 32, 2, 2)
+    assert mcke.gemm_mfma_default_tile(1, 1, 1).astuple() == (32, 32, 32, 2, 2)
 
 
 # ---------------------------------------------------------------------------

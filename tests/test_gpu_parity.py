@@ -264,24 +264,28 @@ def test_gemm_512_baseline_config(gpu, orc):
 def test_mfma_kernel_attrs_report_the_whole_tile_kernel(gpu):
     """gemm_kernel_attrs (kernels.hpp:293-302) describes the kernel that whole-tile
     shapes run: the 64x64 tile's direct-to-LDS kernel runs two wave groups (512
-    lanes), the larger tiles one (256 lanes)."""
+    lanes), the larger tiles one (256 lanes), the 32x32 tile four one-wave groups
+    (256 lanes)."""
     T = gpu.GemmTile
-    for tile, threads in ((T(64, 64, 32, 4, 4), 512), (T(128, 128, 32, 8, 8), 256),
-                          (T(256, 256, 32, 16, 16), 256)):
+    for tile, threads in ((T(32, 32, 32, 2, 2), 256), (T(64, 64, 32, 4, 4), 512),
+                          (T(128, 128, 32, 8, 8), 256), (T(256, 256, 32, 16, 16), 256)):
         st, at = gpu.gemm_kernel_attrs(gpu.GemmVariant.kMfmaF32, tile)
         assert st.ok(), str(st)
         assert at.threads_per_block == threads, tile.astuple()
         assert at.max_blocks_per_sm_api >= 1 and at.local_bytes == 0, tile.astuple()
 
 
-@pytest.mark.parametrize("n", [64, 192, 512, 1024])
-def test_gemm_64_tile_two_wave_groups(gpu, orc, n):
-    """The 64x64 whole-tile kernel folds its two wave groups' K halves in a fixed
-    order: the full reference (reference.hpp:199-211) at the K-scaled tolerance,
-    the same bits on a second launch, and beta = 0 never reading a NaN-poisoned C."""
+@pytest.mark.parametrize("tile", [(64, 64, 32, 4, 4), (32, 32, 32, 2, 2)])
+@pytest.mark.parametrize("n", [32, 64, 192, 512, 1024, 100, 257])
+def test_gemm_wave_group_tiles(gpu, orc, tile, n):
+    """The 64x64 and 32x32 tiles fold their wave groups' shares of K in a fixed
+    order (whole tiles on the direct-to-LDS kernel; n = 100 and 257 on the staged
+    kernel, whose 32x32 tile also runs four groups): the full reference
+    (reference.hpp:199-211) at the K-scaled tolerance, the same bits on a second
+    launch, and beta = 0 never reading a NaN-poisoned C."""
     a = orc.fill_random(n * n, 0x6E33A + n)
     b = orc.fill_random(n * n, 0x8B10C + n)
-    t = gpu.GemmTile(64, 64, 32, 4, 4)
+    t = gpu.GemmTile(*tile)
     want = orc.gemm(a, b, np.zeros(n * n, np.float32), n, n, n)
     poisoned = np.full(n * n, np.nan, np.float32)
     got = run_gemm(gpu, a, b, poisoned, n, n, n, 1.0, 0.0, gpu.GemmVariant.kMfmaF32, t)
