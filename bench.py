@@ -380,13 +380,36 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     out["stream_copy_gb_s"] = round(2 * nt * 4 / (ms * 1e-3) / 1e9, 1)
     if not np.all(arrs[1][2].download(16) == 1.0):
         raise RuntimeError("stream copy produced wrong values")
+    # The same copy at the size of the two ~33.5 MB ops (softmax 32768x128, bias+GELU
+    # 4096x1024): 16 MiB in + 16 MiB out over 24 rotating sets (805 MB per rotation,
+    # 3x the Infinity Cache), back to back.  At this size a launch's ramp and drain
+    # weigh as much as its transfer, so this, not the 256 MiB copy, is those ops'
+    # read+write ceiling.
+    ns, nsets = 1 << 22, 24
+    small = [(D.from_array(np.full(ns, 1.0, np.float32)), D(ns * 4)) for _ in range(nsets)]
+    for s in range(nsets):
+        ck(m.launch_stream_copy_f32(small[s][0], small[s][1], ns, stream))
+    reps_small = 10 * nsets
+    e0.record(stream)
+    for s in range(reps_small):
+        m.launch_stream_copy_f32(small[s % nsets][0], small[s % nsets][1], ns, stream)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1) / reps_small
+    out["stream_copy_32mib_gb_s"] = round(2 * ns * 4 / (ms * 1e-3) / 1e9, 1)
+    if not np.all(small[-1][1].download(16) == 1.0):
+        raise RuntimeError("small stream copy produced wrong values")
+    del small
     out["note"] = ("mfma: blocks = 2 x CUs, 4 waves each, 4 chains of v_mfma_f32_32x32x2_f32, "
                    f"{mfma_iters} iterations (~GEMM launch length); triad: a = 3c + b over "
                    "3 x 256 MiB, two rotating sets; copy: y = x over 2 x 256 MiB, one float4 "
                    "per lane, non-temporal, two rotating sets (the 1-read + 1-write ceiling "
-                   "of softmax and bias+act, frac_of_copy)")
+                   "of softmax and bias+act, frac_of_copy); copy_32mib: the same copy of "
+                   "16 MiB in + 16 MiB out over 24 rotating sets (the ceiling of the two "
+                   "~33.5 MB ops)")
     log(f"measured peaks: MFMA fp32 {out['mfma_f32_tflops']} TFLOP/s, "
-        f"triad {out['stream_triad_gb_s']} GB/s, copy {out['stream_copy_gb_s']} GB/s")
+        f"triad {out['stream_triad_gb_s']} GB/s, copy {out['stream_copy_gb_s']} GB/s, "
+        f"copy at 32 MiB {out['stream_copy_32mib_gb_s']} GB/s")
     return out
 
 
@@ -470,16 +493,21 @@ def gemm_lp_section(m, stream, iters=10, with_peak=True):
             bufs[key] = (D.from_array(ha16), D.from_array(hb16), ha16, hb16)
         return bufs[key]
 
-    def time_launch(fn):
-        for _ in range(3):
-            fn()
+    def batch(fn, count):
         e0, e1 = m.Event(), m.Event()
         e0.record(stream)
-        for _ in range(iters):
+        for _ in range(count):
             fn()
         e1.record(stream)
         stream.synchronize()
-        return e0.elapsed_ms(e1) / iters
+        return e0.elapsed_ms(e1) / count
+
+    def time_launch(fn, warm_ms=150.0, timed_ms=40.0):
+        """Steady clock, as in gemm_sweep: about `warm_ms` of launches first, then
+        at least `iters` launches covering about `timed_ms`."""
+        est = batch(fn, 3)
+        batch(fn, max(1, int(warm_ms / max(est, 1e-3))))
+        return batch(fn, max(iters, int(timed_ms / max(est, 1e-3))))
 
     cases = [(8192, DT.kBF16, DT.kBF16), (8192, DT.kBF16, DT.kF32), (8192, DT.kF16, DT.kF16),
              (8192, DT.kF16, DT.kF32), (4096, DT.kBF16, DT.kBF16), (2048, DT.kBF16, DT.kBF16),
@@ -856,7 +884,10 @@ def main(argv=None) -> int:
     traffic = profiled_traffic()
     summaries = []
     for op in ops:
-        op.copy_peak = peaks["stream_copy_gb_s"] if peaks else None
+        if peaks:
+            # Ops of a few tens of MB are held to the copy of their own size.
+            op.copy_peak = (peaks["stream_copy_32mib_gb_s"] if op.work < 64e6
+                            else peaks["stream_copy_gb_s"])
         mp = None
         if peaks:
             mp = peaks["mfma_f32_tflops"] if op.bound == "mfma" else peaks["stream_triad_gb_s"]
