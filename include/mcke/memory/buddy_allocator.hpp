@@ -70,6 +70,12 @@ class BuddyAllocator : public DeviceAllocator {
   // Memory seams (tests substitute host memory through these).
   [[nodiscard]] virtual StatusOr<void*> raw_alloc(std::size_t bytes);
   virtual void raw_free(void* p);
+  // Waits for the streams of parked blocks, then returns every slab and bypass
+  // allocation through raw_free; idempotent.  The destructor calls it, but a
+  // virtual call from a base destructor reaches the base's own seams, so a
+  // subclass that overrides wait_stream or raw_free must call release_all() from
+  // its own destructor.
+  void release_all() noexcept;
 
  private:
   struct Slab {

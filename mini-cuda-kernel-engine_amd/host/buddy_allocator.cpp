@@ -25,7 +25,9 @@ BuddyAllocator::BuddyAllocator(BuddyConfig cfg) : cfg_(cfg) {
   if (cfg_.growth_factor < 1.0) cfg_.growth_factor = 1.0;
 }
 
-BuddyAllocator::~BuddyAllocator() {
+BuddyAllocator::~BuddyAllocator() { release_all(); }
+
+void BuddyAllocator::release_all() noexcept {
   // Work that still uses parked blocks must finish before the slabs go away.
   for (const Parked& p : parked_) wait_stream(p.stream);
   parked_.clear();

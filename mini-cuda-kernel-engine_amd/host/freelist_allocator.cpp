@@ -28,7 +28,9 @@ FreeListAllocator::FreeListAllocator(FreeListConfig cfg) : cfg_(cfg) {
   cache_.resize(size_class_of(cfg_.large_alloc_threshold) + 1);
 }
 
-FreeListAllocator::~FreeListAllocator() {
+FreeListAllocator::~FreeListAllocator() { release_all(); }
+
+void FreeListAllocator::release_all() noexcept {
   // Work that still uses parked blocks must finish before the slabs go away.
   for (const Parked& p : parked_) wait_stream(p.stream);
   parked_.clear();

@@ -497,6 +497,8 @@ TEST(memory_and_schedule_fuzz_random_dags) {
 class HostBuddy : public BuddyAllocator {
  public:
   using BuddyAllocator::BuddyAllocator;
+  // The base destructor would reach the base seams (hipFree on host memory).
+  ~HostBuddy() override { release_all(); }
   mutable std::set<rt::StreamHandle> busy;
   int raw_allocs = 0, raw_frees = 0;
 
@@ -523,6 +525,80 @@ static BuddyConfig small_cfg(ReusePolicy p) {
   c.large_alloc_threshold = 4 << 20;
   c.reuse_policy = p;
   return c;
+}
+
+// Destruction returns every slab and bypass allocation through the subclass's
+// own memory seam, and waits for parked blocks' streams through its own
+// completion seam (release_all() from the subclass destructor).
+struct SeamLedger {
+  int allocs = 0, frees = 0, waits = 0;
+};
+class LedgerBuddy : public BuddyAllocator {
+ public:
+  LedgerBuddy(BuddyConfig c, SeamLedger* l) : BuddyAllocator(c), l_(l) {}
+  ~LedgerBuddy() override { release_all(); }
+
+ protected:
+  bool stream_completed(rt::StreamHandle) const override { return false; }
+  void wait_stream(rt::StreamHandle) const override { ++l_->waits; }
+  StatusOr<void*> raw_alloc(std::size_t bytes) override {
+    ++l_->allocs;
+    return std::aligned_alloc(256, bytes);
+  }
+  void raw_free(void* p) override {
+    ++l_->frees;
+    std::free(p);
+  }
+
+ private:
+  SeamLedger* l_;
+};
+class LedgerFreeList : public FreeListAllocator {
+ public:
+  LedgerFreeList(FreeListConfig c, SeamLedger* l) : FreeListAllocator(c), l_(l) {}
+  ~LedgerFreeList() override { release_all(); }
+
+ protected:
+  bool stream_completed(rt::StreamHandle) const override { return false; }
+  void wait_stream(rt::StreamHandle) const override { ++l_->waits; }
+  StatusOr<void*> raw_alloc(std::size_t bytes) override {
+    ++l_->allocs;
+    return std::aligned_alloc(256, bytes);
+  }
+  void raw_free(void* p) override {
+    ++l_->frees;
+    std::free(p);
+  }
+
+ private:
+  SeamLedger* l_;
+};
+
+TEST(allocators_release_through_subclass_seams) {
+  SeamLedger lb;
+  {
+    LedgerBuddy b(small_cfg(ReusePolicy::kCoarseStreamPoll), &lb);
+    auto a = b.allocate(1000, fake_stream(1));
+    auto big = b.allocate(8 << 20, fake_stream(1));     // above the threshold: bypass
+    CHECK(a.ok() && big.ok());
+    CHECK_OK(b.deallocate(*a, fake_stream(1)));          // parked: its stream never completes
+  }
+  CHECK_EQ(lb.allocs, 2);
+  CHECK_EQ(lb.frees, 2);
+  CHECK(lb.waits >= 1);
+  SeamLedger lf;
+  {
+    FreeListConfig c;
+    c.slab_bytes = 1 << 20;
+    LedgerFreeList f(c, &lf);
+    CHECK_OK(f.config_status());
+    auto a = f.allocate(1000, fake_stream(2));
+    CHECK(a.ok());
+    CHECK_OK(f.deallocate(*a, fake_stream(2)));
+  }
+  CHECK(lf.allocs >= 1);
+  CHECK_EQ(lf.frees, lf.allocs);
+  CHECK(lf.waits >= 1);
 }
 
 TEST(buddy_sizes_split_merge_validate) {
@@ -622,6 +698,8 @@ TEST(buddy_growth_bypass_and_trim) {
 class HostFreeList : public FreeListAllocator {
  public:
   using FreeListAllocator::FreeListAllocator;
+  // The base destructor would reach the base seams (hipFree on host memory).
+  ~HostFreeList() override { release_all(); }
   mutable std::set<rt::StreamHandle> busy;
   int raw_allocs = 0, raw_frees = 0;
 
