@@ -946,7 +946,8 @@ def main(argv=None) -> int:
                         "8192x8192, full sum 2^26, softmax 32768x{128,1024,4096}, "
                         "bias+GELU_tanh 16384x4096 and 4096x1024",
             "gemm_tile": list(m.gemm_mfma_default_tile(8192, 8192, 8192).astuple()),
-            "device": info.name.decode(),
+            # The runtime leaves the marketing name empty on some boxes.
+            "device": info.name.decode() or f"{info.arch.decode()} ({info.sm_count} CUs)",
         },
         "roofline": {
             "bound": gemm["bound"], "achieved": gemm["achieved"], "peak": gemm["peak"],
