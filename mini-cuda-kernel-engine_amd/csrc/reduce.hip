@@ -40,13 +40,16 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kLoadUnroll = 4;      // loads in flight per lane, one-pass kernels
-// kTwoPass sizing: one workgroup per CU on a 256-CU part, each lane keeping 8
-// float4 loads in flight.  Measured on the full-tensor sum of 2^26 floats (one
-// launch, fold by the last arrival): 41.0 us at 256 x 8, 42.5 us at 512 x 8,
-// 44.9 us at 1024 x 8, 50.3 us at 2048 x 8, and 54.5 us at 256 x 4 -- each
-// workgroup ends with a round trip (its partial's store, then the arrival
-// count) during which its slot issues no loads, so fewer, longer workgroups win.
-constexpr int kPass1Unroll = 8;
+// kTwoPass sizing: one 512-lane workgroup per CU on a 256-CU part, each lane
+// keeping 4 float4 loads in flight.  Measured on the full-tensor sum of 2^26
+// floats (one launch, fold by the last arrival), workgroups x lanes x loads:
+// 256 x 512 x 4 40.6 us, 256 x 256 x 8 40.9 us, 256 x 1024 x 2 40.9 us,
+// 256 x 1024 x 4 42.9 us, 512 x 256 x 8 42.5 us, 1024 x 256 x 8 44.9 us,
+// 2048 x 256 x 8 50.3 us -- each workgroup ends with a round trip (its partial's
+// store, then the arrival count) during which its slot issues no loads, so few,
+// wide workgroups win.
+constexpr int kSplitThreads = 512;
+constexpr int kPass1Unroll = 4;
 constexpr int64_t kTargetBlocks = 256;
 constexpr int64_t kMinColsPerBlock = 4096;
 constexpr int64_t kMaxSplit = 65535;
@@ -81,52 +84,52 @@ template <class Op> __device__ __forceinline__ float fold4(f32x4 v) {
   return Op::apply(Op::apply(v[0], v[1]), Op::apply(v[2], v[3]));
 }
 
-// Partial of x[begin, end) for this thread, lanes striding by kThreads.
+// Partial of x[begin, end) for this thread, NT lanes striding through it.
 // VEC: begin and end are multiples of 4 and x is 16-byte aligned.
-template <class Op, bool VEC, int U = kLoadUnroll>
+template <class Op, bool VEC, int U = kLoadUnroll, int NT = kThreads>
 __device__ __forceinline__ float thread_partial(const float* __restrict__ x, int64_t begin,
                                                 int64_t end) {
   float acc = Op::identity();
   if constexpr (VEC) {
     const f32x4* __restrict__ xv = reinterpret_cast<const f32x4*>(x);
     const int64_t b4 = begin >> 2, e4 = end >> 2;
-    for (int64_t i = b4 + threadIdx.x; i < e4; i += U * kThreads) {
+    for (int64_t i = b4 + threadIdx.x; i < e4; i += U * NT) {
       f32x4 a[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t j = i + u * kThreads;
+        const int64_t j = i + u * NT;
         if (j < e4) a[u] = ld_stream(xv + j);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (i + u * kThreads < e4) acc = Op::apply(acc, fold4<Op>(a[u]));
+        if (i + u * NT < e4) acc = Op::apply(acc, fold4<Op>(a[u]));
     }
   } else {
-    for (int64_t i = begin + threadIdx.x; i < end; i += U * kThreads) {
+    for (int64_t i = begin + threadIdx.x; i < end; i += U * NT) {
       float a[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t j = i + u * kThreads;
+        const int64_t j = i + u * NT;
         if (j < end) a[u] = ld_stream(x + j);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (i + u * kThreads < end) acc = Op::apply(acc, a[u]);
+        if (i + u * NT < end) acc = Op::apply(acc, a[u]);
     }
   }
   return acc;
 }
 
-// Workgroup combine, wave64 butterfly + one LDS stage.  Valid in every lane.
-template <class Op> __device__ __forceinline__ float block_combine_shfl(float v) {
-  __shared__ float part[kThreads / kWave];
+// Workgroup combine (NT lanes), wave64 butterfly + one LDS stage.  Valid in every lane.
+template <class Op, int NT = kThreads> __device__ __forceinline__ float block_combine_shfl(float v) {
+  __shared__ float part[NT / kWave];
   v = Op::wave(v);
   const int w = threadIdx.x / kWave;
   if ((threadIdx.x % kWave) == 0) part[w] = v;
   __syncthreads();
   float r = part[0];
 #pragma unroll
-  for (int i = 1; i < kThreads / kWave; ++i) r = Op::apply(r, part[i]);
+  for (int i = 1; i < NT / kWave; ++i) r = Op::apply(r, part[i]);
   return r;
 }
 
@@ -161,7 +164,7 @@ __global__ __launch_bounds__(kThreads) void row_reduce_kernel(const float* __res
 // stage should not add error on top of the first.  COHERENT reads the partials
 // with device-scope loads (they were written by other workgroups of the same
 // launch, possibly on another XCD, whose L2 this one does not share).
-template <class Op, bool MEAN, bool COHERENT>
+template <class Op, bool MEAN, bool COHERENT, int NT = kThreads>
 __device__ __forceinline__ float fold_partials(const float* p, int64_t split, int64_t cols) {
   auto get = [&](int64_t i) -> float {
     if constexpr (COHERENT)
@@ -171,21 +174,21 @@ __device__ __forceinline__ float fold_partials(const float* p, int64_t split, in
   };
   const int w = threadIdx.x / kWave;
   if constexpr (std::is_same_v<Op, SumOp>) {
-    __shared__ double part[kThreads / kWave];
+    __shared__ double part[NT / kWave];
     double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < split; i += kThreads) acc += static_cast<double>(get(i));
+    for (int64_t i = threadIdx.x; i < split; i += NT) acc += static_cast<double>(get(i));
 #pragma unroll
     for (int m = kWave / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
     if ((threadIdx.x % kWave) == 0) part[w] = acc;
     __syncthreads();
     double t = part[0];
 #pragma unroll
-    for (int i = 1; i < kThreads / kWave; ++i) t += part[i];
+    for (int i = 1; i < NT / kWave; ++i) t += part[i];
     return static_cast<float>(MEAN ? t / static_cast<double>(cols) : t);
   } else {
     float acc = Op::identity();
-    for (int64_t i = threadIdx.x; i < split; i += kThreads) acc = Op::apply(acc, get(i));
-    return block_combine_shfl<Op>(acc);
+    for (int64_t i = threadIdx.x; i < split; i += NT) acc = Op::apply(acc, get(i));
+    return block_combine_shfl<Op, NT>(acc);
   }
 }
 
@@ -205,7 +208,7 @@ __device__ __forceinline__ float fold_partials(const float* p, int64_t split, in
 // workgroup (measured: the launch takes 49 us instead of 41 us at 256
 // workgroups), and only the partial needs publishing.
 template <class Op, bool VEC, bool MEAN>
-__global__ __launch_bounds__(kThreads) void row_reduce_split_kernel(
+__global__ __launch_bounds__(kSplitThreads) void row_reduce_split_kernel(
     const float* __restrict__ x, float* __restrict__ ws, float* __restrict__ out, int64_t cols,
     int64_t chunk, int64_t split, int counter_base) {
   const int64_t s = blockIdx.x;
@@ -214,8 +217,8 @@ __global__ __launch_bounds__(kThreads) void row_reduce_split_kernel(
   int64_t end = begin + chunk;
   if (end > cols) end = cols;
   float v = Op::identity();
-  if (begin < end) v = thread_partial<Op, VEC, kPass1Unroll>(x + r * cols, begin, end);
-  v = block_combine_shfl<Op>(v);
+  if (begin < end) v = thread_partial<Op, VEC, kPass1Unroll, kSplitThreads>(x + r * cols, begin, end);
+  v = block_combine_shfl<Op, kSplitThreads>(v);
   if (split == 1) {
     if (threadIdx.x == 0) out[r] = MEAN ? v / static_cast<float>(cols) : v;
     return;
@@ -238,17 +241,18 @@ __global__ __launch_bounds__(kThreads) void row_reduce_split_kernel(
   }
   __syncthreads();
   if (!last) return;
-  const float t = fold_partials<Op, MEAN, true>(ws + r * split, split, cols);
+  const float t = fold_partials<Op, MEAN, true, kSplitThreads>(ws + r * split, split, cols);
   if (threadIdx.x == 0) out[r] = t;
 }
 
 // The fold as a launch of its own (one workgroup per row), for kTwoPass launches
-// that have no counter block.
+// that have no counter block.  Same lane count and order as the last arrival's
+// fold, so both paths give the same bits.
 template <class Op, bool MEAN>
-__global__ __launch_bounds__(kThreads) void row_reduce_fold_kernel(
+__global__ __launch_bounds__(kSplitThreads) void row_reduce_fold_kernel(
     const float* __restrict__ ws, float* __restrict__ out, int64_t split, int64_t cols) {
   const int64_t r = blockIdx.x;
-  const float t = fold_partials<Op, MEAN, false>(ws + r * split, split, cols);
+  const float t = fold_partials<Op, MEAN, false, kSplitThreads>(ws + r * split, split, cols);
   if (threadIdx.x == 0) out[r] = t;
 }
 
@@ -317,14 +321,15 @@ int launch_two_pass(const float* x, float* out, int64_t rows, int64_t cols, floa
   }
   const dim3 g1(static_cast<unsigned>(split), static_cast<unsigned>(rows), 1u);
   if (vec)
-    row_reduce_split_kernel<Op, true, MEAN><<<g1, kThreads, 0, st>>>(x, ws, out, cols, chunk,
-                                                                     split, counter_base);
+    row_reduce_split_kernel<Op, true, MEAN><<<g1, kSplitThreads, 0, st>>>(x, ws, out, cols, chunk,
+                                                                          split, counter_base);
   else
-    row_reduce_split_kernel<Op, false, MEAN><<<g1, kThreads, 0, st>>>(x, ws, out, cols, chunk,
-                                                                      split, counter_base);
+    row_reduce_split_kernel<Op, false, MEAN><<<g1, kSplitThreads, 0, st>>>(x, ws, out, cols,
+                                                                           chunk, split,
+                                                                           counter_base);
   MCKE_LAUNCH_CHECK("row_reduce_split_kernel");
   if (split > 1 && counter_base < 0) {
-    row_reduce_fold_kernel<Op, MEAN><<<static_cast<unsigned>(rows), kThreads, 0, st>>>(
+    row_reduce_fold_kernel<Op, MEAN><<<static_cast<unsigned>(rows), kSplitThreads, 0, st>>>(
         ws, out, split, cols);
     MCKE_LAUNCH_CHECK("row_reduce_fold_kernel");
   }
