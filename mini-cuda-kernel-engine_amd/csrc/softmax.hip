@@ -39,7 +39,9 @@ __device__ __forceinline__ float exp_le0(float t) {
 }
 
 // ---------------------------------------------------------------------------
-// Register-resident rows.  TPR lanes per row (8, 16, 64 or 256), VPT float4 per lane.
+// Register-resident rows.  NT-lane workgroups, TPR lanes per row (8 .. 512), VPT
+// float4 per lane.  A row wider than a wave spans TPR / 64 consecutive waves,
+// combined through one LDS stage over that row's own waves.
 // ---------------------------------------------------------------------------
 template <int TPR> __device__ __forceinline__ float group_max(float v, float* lds) {
   if constexpr (TPR <= kWave) {
@@ -47,11 +49,12 @@ template <int TPR> __device__ __forceinline__ float group_max(float v, float* ld
   } else {
     v = wave_max<kWave>(v);
     const int w = threadIdx.x / kWave;
+    const int first = (threadIdx.x / TPR) * (TPR / kWave);   // the row's first wave
     if ((threadIdx.x % kWave) == 0) lds[w] = v;
     __syncthreads();
-    float r = lds[0];
+    float r = lds[first];
 #pragma unroll
-    for (int i = 1; i < TPR / kWave; ++i) r = fmaxf(r, lds[i]);
+    for (int i = 1; i < TPR / kWave; ++i) r = fmaxf(r, lds[first + i]);
     __syncthreads();   // lds is reused by group_sum
     return r;
   }
@@ -63,22 +66,23 @@ template <int TPR> __device__ __forceinline__ float group_sum(float v, float* ld
   } else {
     v = wave_sum<kWave>(v);
     const int w = threadIdx.x / kWave;
+    const int first = (threadIdx.x / TPR) * (TPR / kWave);
     if ((threadIdx.x % kWave) == 0) lds[w] = v;
     __syncthreads();
-    float r = lds[0];
+    float r = lds[first];
 #pragma unroll
-    for (int i = 1; i < TPR / kWave; ++i) r += lds[i];
+    for (int i = 1; i < TPR / kWave; ++i) r += lds[first + i];
     return r;
   }
 }
 
-template <int TPR, int VPT>
-__global__ __launch_bounds__(kThreads) void softmax_regs_kernel(const float* __restrict__ x,
-                                                                float* __restrict__ y,
-                                                                int64_t rows, int64_t cols) {
-  static_assert(kThreads % TPR == 0, "TPR must divide the workgroup");
-  constexpr int kRowsPerBlock = kThreads / TPR;
-  __shared__ float lds[kThreads / kWave];
+template <int TPR, int VPT, int NT = kThreads>
+__global__ __launch_bounds__(NT) void softmax_regs_kernel(const float* __restrict__ x,
+                                                          float* __restrict__ y, int64_t rows,
+                                                          int64_t cols) {
+  static_assert(NT % TPR == 0, "TPR must divide the workgroup");
+  constexpr int kRowsPerBlock = NT / TPR;
+  __shared__ float lds[NT / kWave];
   const int t = threadIdx.x % TPR;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
   // Rows past the end still take part in the barriers of a multi-wave group,
@@ -215,11 +219,11 @@ __global__ __launch_bounds__(kThreads) void softmax_three_pass_kernel(
     y[base + c] = exp_le0(x[base + c] - m) * inv;
 }
 
-template <int TPR, int VPT>
+template <int TPR, int VPT, int NT = kThreads>
 int launch_regs(const float* x, float* y, int64_t rows, int64_t cols, hipStream_t s) {
-  constexpr int rpb = kThreads / TPR;
+  constexpr int rpb = NT / TPR;
   const int64_t g = (rows + rpb - 1) / rpb;
-  softmax_regs_kernel<TPR, VPT><<<static_cast<unsigned>(g), kThreads, 0, s>>>(x, y, rows, cols);
+  softmax_regs_kernel<TPR, VPT, NT><<<static_cast<unsigned>(g), NT, 0, s>>>(x, y, rows, cols);
   MCKE_LAUNCH_CHECK("softmax_regs_kernel");
   return ok();
 }
@@ -232,12 +236,17 @@ int launch_online(const float* x, float* y, int64_t rows, int64_t cols, hipStrea
     // Short rows: fewer lanes per row and four float4s per lane, so a launch at
     // 32768 rows is one round of resident workgroups with 64 bytes per lane in
     // flight (measured 6.2 us vs 8.2 us for one float4 per lane at 128 columns).
+    // Longer rows: two float4s per lane over more lanes.  At 32768 x 1024, 128
+    // lanes x 2 took 42.9 us (64 x 4: 43.4, 32 x 8: 44.5, 256 x 1: 45.1; a plain
+    // copy of the same bytes 42.7); at 32768 x 4096, 512-lane workgroups of one
+    // row x 2 took 163.2 us (256 x 4: 172.9, 128 x 8: 178.0, 64 x 16: 181.4; the
+    // copy 165.5).
     if (cv <= 32) return launch_regs<8, 4>(x, y, rows, cols, s);
     if (cv <= 64) return launch_regs<16, 4>(x, y, rows, cols, s);
     if (cv <= 128) return launch_regs<64, 2>(x, y, rows, cols, s);
-    if (cv <= 256) return launch_regs<64, 4>(x, y, rows, cols, s);
+    if (cv <= 256) return launch_regs<128, 2>(x, y, rows, cols, s);
     if (cv <= 512) return launch_regs<64, 8>(x, y, rows, cols, s);
-    if (cv <= 1024) return launch_regs<256, 4>(x, y, rows, cols, s);
+    if (cv <= 1024) return launch_regs<512, 2, 512>(x, y, rows, cols, s);
     return launch_regs<256, 8>(x, y, rows, cols, s);
   }
   softmax_online_kernel<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(x, y, cols);
