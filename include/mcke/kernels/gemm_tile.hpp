@@ -5,8 +5,10 @@
 // the constants of gfx950 instead of sm_75:
 //   * a tile's lane count must be a multiple of the 64-lane wavefront;
 //   * GemmVariant is append-only and gains kMfmaF32 (= 8), whose tiles are
-//     (256,256,32,16,16), (256,256,16,16,16), (128,128,32,8,8), (128,128,16,8,8)
-//     and (64,64,32,4,4): 256 lanes, tm x tn accumulators per lane;
+//     (256,256,32,16,16), (256,256,16,16,16), (128,128,32,8,8), (128,128,16,8,8),
+//     (64,64,32,4,4) and (32,32,32,2,2): 256 lanes in the (bm/tm) x (bn/tn)
+//     descriptor (the whole-tile kernels of the two smallest tiles split each
+//     K stage over wave groups; the descriptor stays the tile's identity);
 //   * occupancy is limited per SIMD by the 512-entry unified VGPR file (arch +
 //     accumulation registers, allocated in granules of 8) and 8 waves, per CU by
 //     160 KiB of LDS, the 2048-lane cap and the workgroup cap.
@@ -73,6 +75,7 @@ enum class GemmTileConfig : std::uint8_t {
   kMfma128x128x32,
   kMfma128x128x16,
   kMfma64x64x32,
+  kMfma32x32x32,
 };
 
 [[nodiscard]] constexpr GemmTileConfig select_tile_config(const GemmTile& t) {
@@ -87,6 +90,7 @@ enum class GemmTileConfig : std::uint8_t {
     if (t.bk == 16) return GemmTileConfig::kMfma128x128x16;
   }
   if (t.bm == 64 && t.bn == 64 && t.bk == 32 && t.tm == 4 && t.tn == 4) return GemmTileConfig::kMfma64x64x32;
+  if (t.bm == 32 && t.bn == 32 && t.bk == 32 && t.tm == 2 && t.tn == 2) return GemmTileConfig::kMfma32x32x32;
   return GemmTileConfig::kUnsupported;
 }
 
@@ -110,7 +114,7 @@ enum class GemmVariant : std::uint8_t {
 [[nodiscard]] constexpr bool is_mfma_config(GemmTileConfig c) {
   return c == GemmTileConfig::kMfma256x256x32 || c == GemmTileConfig::kMfma256x256x16 ||
          c == GemmTileConfig::kMfma128x128x32 || c == GemmTileConfig::kMfma128x128x16 ||
-         c == GemmTileConfig::kMfma64x64x32;
+         c == GemmTileConfig::kMfma64x64x32 || c == GemmTileConfig::kMfma32x32x32;
 }
 
 // The instantiation a tile-using variant requires (for kMfmaF32 any MFMA config).

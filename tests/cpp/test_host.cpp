@@ -65,13 +65,17 @@ TEST(gemm_tile_validity_wave64) {
   CHECK(!K::tile_is_self_consistent(K::GemmTile{100, 128, 8, 8, 8}));      // 100 % 8 != 0
   for (const auto& t : {K::GemmTile{256, 256, 32, 16, 16}, K::GemmTile{256, 256, 16, 16, 16},
                         K::GemmTile{128, 128, 32, 8, 8}, K::GemmTile{128, 128, 16, 8, 8},
-                        K::GemmTile{64, 64, 32, 4, 4}}) {
+                        K::GemmTile{64, 64, 32, 4, 4}, K::GemmTile{32, 32, 32, 2, 2}}) {
     CHECK(K::tile_is_self_consistent(t));
     CHECK_EQ(K::threads_per_block(t), 256);
     CHECK(K::gemm_tile_is_supported(K::GemmVariant::kMfmaF32, t));
     CHECK(!K::gemm_tile_is_supported(K::GemmVariant::kWarpTile, t));
   }
   CHECK(!K::gemm_tile_is_supported(K::GemmVariant::kMfmaF32, K::GemmTile{}));
+  CHECK(!K::gemm_tile_is_supported(K::GemmVariant::kMfmaF32, K::GemmTile{32, 32, 16, 2, 2}));
+  // The launcher's default tile is always one the host model accepts.
+  for (std::int64_t n : {1, 100, 256, 512, 1024, 3072, 4096, 6144, 8192})
+    CHECK(K::gemm_tile_is_supported(K::GemmVariant::kMfmaF32, K::mfma_default_tile(n, n, n)));
   CHECK(K::gemm_tile_is_supported(K::GemmVariant::kWarpTile, K::GemmTile{}));
   CHECK(!K::gemm_tile_is_supported(K::GemmVariant::kTiledSmem, K::GemmTile{}));
   CHECK(K::gemm_tile_is_supported(K::GemmVariant::kTiledSmem, K::GemmTile{32, 32, 32, 1, 1}));
