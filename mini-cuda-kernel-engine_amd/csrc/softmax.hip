@@ -39,7 +39,7 @@ __device__ __forceinline__ float exp_le0(float t) {
 }
 
 // ---------------------------------------------------------------------------
-// Register-resident rows.  NT-lane workgroups, TPR lanes per row (8 .. 512), VPT
+// Register-resident rows.  NT-lane workgroups, TPR lanes per row (8 .. 1024), VPT
 // float4 per lane.  A row wider than a wave spans TPR / 64 consecutive waves,
 // combined through one LDS stage over that row's own waves.
 // ---------------------------------------------------------------------------
@@ -240,14 +240,15 @@ int launch_online(const float* x, float* y, int64_t rows, int64_t cols, hipStrea
     // lanes x 2 took 42.9 us (64 x 4: 43.4, 32 x 8: 44.5, 256 x 1: 45.1; a plain
     // copy of the same bytes 42.7); at 32768 x 4096, 512-lane workgroups of one
     // row x 2 took 163.2 us (256 x 4: 172.9, 128 x 8: 178.0, 64 x 16: 181.4; the
-    // copy 165.5).
+    // copy 165.5); at 16384 x 8192, 1024-lane workgroups of one row x 2 took
+    // 171.0 us (256 x 8: 176.5, 512 x 4: 187.2).
     if (cv <= 32) return launch_regs<8, 4>(x, y, rows, cols, s);
     if (cv <= 64) return launch_regs<16, 4>(x, y, rows, cols, s);
     if (cv <= 128) return launch_regs<64, 2>(x, y, rows, cols, s);
     if (cv <= 256) return launch_regs<128, 2>(x, y, rows, cols, s);
     if (cv <= 512) return launch_regs<64, 8>(x, y, rows, cols, s);
     if (cv <= 1024) return launch_regs<512, 2, 512>(x, y, rows, cols, s);
-    return launch_regs<256, 8>(x, y, rows, cols, s);
+    return launch_regs<1024, 2, 1024>(x, y, rows, cols, s);
   }
   softmax_online_kernel<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(x, y, cols);
   MCKE_LAUNCH_CHECK("softmax_online_kernel");
