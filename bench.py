@@ -351,9 +351,13 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     ms = e0.elapsed_ms(e1) / iters
     out["mfma_f32_tflops"] = round(m.mfma_peak_flops(blocks, mfma_iters) / (ms * 1e-3) / 1e12, 2)
     out["mfma_f32_launch_ms"] = round(ms, 4)
+    # Random operands, like the ops' own inputs: HBM moves constant data measurably
+    # faster (a 256 MiB copy of zeros took 79.7 us against 82.5-85 us for varied
+    # data on one box), which would inflate the ceilings the ops are held to.
     nt = 1 << 26
-    arrs = [(D.from_array(np.full(nt, 1.0, np.float32)), D.from_array(np.full(nt, 2.0, np.float32)),
-             D(nt * 4)) for _ in range(2)]
+    hb = m.fill_random(nt, 0x7A1AD, 0.0, 1.0)
+    hc = m.fill_random(nt, 0x7A1AE, 0.0, 1.0)
+    arrs = [(D.from_array(hb), D.from_array(hc), D(nt * 4)) for _ in range(2)]
     for s in range(2):
         ck(m.launch_stream_triad_f32(arrs[s][0], arrs[s][1], arrs[s][2], 3.0, nt, stream))
     reps = 20
@@ -366,8 +370,9 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     ms = e0.elapsed_ms(e1) / reps
     out["stream_triad_gb_s"] = round(3 * nt * 4 / (ms * 1e-3) / 1e9, 1)
     got = arrs[1][2].download(16)
-    if not np.all(got == 7.0):
-        raise RuntimeError(f"stream triad produced {got[:4]}, expected 7.0")
+    want = (np.float32(3.0) * hc[:16] + hb[:16]).astype(np.float32)
+    if not np.allclose(got, want, rtol=1e-6, atol=0):
+        raise RuntimeError(f"stream triad produced {got[:4]}, expected {want[:4]}")
     # The read+write ceiling (one read, one write per element), for softmax and bias+act.
     for s in range(2):
         ck(m.launch_stream_copy_f32(arrs[s][0], arrs[s][2], nt, stream))
@@ -378,7 +383,7 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     stream.synchronize()
     ms = e0.elapsed_ms(e1) / reps
     out["stream_copy_gb_s"] = round(2 * nt * 4 / (ms * 1e-3) / 1e9, 1)
-    if not np.all(arrs[1][2].download(16) == 1.0):
+    if not np.array_equal(arrs[1][2].download(16), hb[:16]):
         raise RuntimeError("stream copy produced wrong values")
     # The same copy at the size of the two ~33.5 MB ops (softmax 32768x128, bias+GELU
     # 4096x1024): 16 MiB in + 16 MiB out over 24 rotating sets (805 MB per rotation,
@@ -386,7 +391,7 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     # weigh as much as its transfer, so this, not the 256 MiB copy, is those ops'
     # read+write ceiling.
     ns, nsets = 1 << 22, 24
-    small = [(D.from_array(np.full(ns, 1.0, np.float32)), D(ns * 4)) for _ in range(nsets)]
+    small = [(D.from_array(hb[:ns]), D(ns * 4)) for _ in range(nsets)]
     for s in range(nsets):
         ck(m.launch_stream_copy_f32(small[s][0], small[s][1], ns, stream))
     reps_small = 10 * nsets
@@ -397,12 +402,12 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     stream.synchronize()
     ms = e0.elapsed_ms(e1) / reps_small
     out["stream_copy_32mib_gb_s"] = round(2 * ns * 4 / (ms * 1e-3) / 1e9, 1)
-    if not np.all(small[-1][1].download(16) == 1.0):
+    if not np.array_equal(small[-1][1].download(16), hb[:16]):
         raise RuntimeError("small stream copy produced wrong values")
     del small
     out["note"] = ("mfma: blocks = 2 x CUs, 4 waves each, 4 chains of v_mfma_f32_32x32x2_f32, "
                    f"{mfma_iters} iterations (~GEMM launch length); triad: a = 3c + b over "
-                   "3 x 256 MiB, two rotating sets; copy: y = x over 2 x 256 MiB, one float4 "
+                   "3 x 256 MiB of U[0,1) data, two rotating sets; copy: y = x over 2 x 256 MiB, one float4 "
                    "per lane, non-temporal, two rotating sets (the 1-read + 1-write ceiling "
                    "of softmax and bias+act, frac_of_copy); copy_32mib: the same copy of "
                    "16 MiB in + 16 MiB out over 24 rotating sets (the ceiling of the two "
