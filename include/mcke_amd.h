@@ -132,8 +132,8 @@ int mcke_launch_activation_f32(const float* x, float* y, int64_t n, int act,
 int mcke_max_vector_width_f32(const void* p, int64_t cols);
 
 /* row_reduce_workspace_bytes, kernels.hpp:200-202 / reduce.cu:213-218.  Zero for
- * the one-launch variants; kTwoPass needs rows * split * 4 bytes, where this
- * build's split depends on the shape (rows and cols). */
+ * kSmemTree and kWarpShuffle; kTwoPass needs rows * split * 4 bytes (the
+ * partials), where this build's split depends on the shape (rows and cols). */
 size_t mcke_row_reduce_workspace_bytes(int64_t rows, int64_t cols, int variant);
 
 /* The frozen 7-argument launch_row_reduce_f32, kernels.hpp:204-207 /
@@ -143,7 +143,11 @@ int mcke_launch_row_reduce_f32(const float* x, float* out, int64_t rows, int64_t
 
 /* The 9-argument launch_row_reduce_f32, kernels.hpp:209-213 / reduce.cu:224-280.
  * out[r] = sum / max / mean of row r (mean = sum / cols).  rows == 1 with
- * kTwoPass is the full-tensor reduction. */
+ * kTwoPass is the full-tensor reduction.  kTwoPass is one launch: the workgroup
+ * that finishes a split row last folds the row's partials, counted on arrival
+ * counters the library keeps per stream (the first 1024 streams; beyond them, or
+ * beyond 256 split rows, two launches with the same result).  The workspace's
+ * contents on entry do not matter. */
 int mcke_launch_row_reduce_ws_f32(const float* x, float* out, int64_t rows, int64_t cols,
                                   int kind, int variant, float* workspace,
                                   size_t workspace_bytes, void* stream);
