@@ -359,3 +359,47 @@ def test_16bit_gemm_node_feeds_f32_ops(G, orc, dt):
     ulp = 2.0 ** -7 if dt == 2 else 2.0 ** -10
     r = orc.compare(got16, want16, orc.tol_gemm(D) + ulp, orc.abs_tol_gemm(D, 4.0 * 0.02 * 4.0))
     assert r.ok, f"gemm_lp 16-bit C: {r}"
+
+
+def test_captured_split_reduce_replays(G, orc):
+    """kTwoPass nodes whose rows split over workgroups, so their one-launch fold
+    runs on the arrival counters of the stream each was captured on; two of them
+    on different streams of one captured graph.  Every replay, also after new
+    inputs, matches the eager launch's bits and the double-accumulating CPU
+    reduce (reference tests/reference.hpp:154-172)."""
+    g = G.Graph()
+    a = g.add_input((2, 65536), "a")
+    b = g.add_input((3, 40000), "b")
+    ra = g.add_reduce(a, "sum_a", kind=0, variant=2)
+    rb = g.add_reduce(b, "mean_b", kind=2, variant=2)
+    g.mark_output(ra)
+    g.mark_output(rb)
+    ex = G.Executor(g, schedule=G.SchedulePolicy.kLevelParallel,
+                    memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=2)
+    ex.plan()
+    assert ex.plan_info()["num_streams_used"] == 2
+    captured = False
+    for rep in range(4):
+        xa = orc.fill_normal(2 * 65536, 0x5A0 + rep, 0.0, 1.0)
+        xb = orc.fill_normal(3 * 40000, 0x5B0 + rep, 0.0, 1.0)
+        ex.set_input(a, xa)
+        ex.set_input(b, xb)
+        if not captured:
+            ex.run_sync()
+            eager = (ex.read(ra, 2).copy(), ex.read(rb, 3).copy())
+            ex.capture()
+            captured = True
+            ex.run_sync()
+            assert np.array_equal(ex.read(ra, 2).view(np.uint32), eager[0].view(np.uint32))
+            assert np.array_equal(ex.read(rb, 3).view(np.uint32), eager[1].view(np.uint32))
+        else:
+            ex.run_sync()
+        for out, x, rows, cols, kind in ((ra, xa, 2, 65536, 0), (rb, xb, 3, 40000, 2)):
+            got = ex.read(out, rows)
+            want = orc.row_reduce(x, rows, cols, kind)
+            floor = 5e-5 * (1.0 / 0.577) * np.sqrt(cols / 4096.0)
+            if kind == 2:
+                floor /= cols
+            r = orc.compare(got, want, 1e-5, floor)
+            assert r.ok, f"replay {rep} kind {kind}: {r}"
+    ex.close()
