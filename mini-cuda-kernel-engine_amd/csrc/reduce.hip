@@ -140,7 +140,8 @@ template <class Op> __device__ __forceinline__ float block_combine_tree(float v)
   __syncthreads();
 #pragma unroll
   for (int s = kThreads / 2; s > 0; s >>= 1) {
-    if (threadIdx.x < s) buf[threadIdx.x] = Op::apply(buf[threadIdx.x], buf[threadIdx.x + s]);
+    if (static_cast<int>(threadIdx.x) < s)
+      buf[threadIdx.x] = Op::apply(buf[threadIdx.x], buf[threadIdx.x + s]);
     __syncthreads();
   }
   return buf[0];
