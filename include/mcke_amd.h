@@ -145,9 +145,10 @@ int mcke_launch_row_reduce_f32(const float* x, float* out, int64_t rows, int64_t
  * out[r] = sum / max / mean of row r (mean = sum / cols).  rows == 1 with
  * kTwoPass is the full-tensor reduction.  kTwoPass is one launch: the workgroup
  * that finishes a split row last folds the row's partials, counted on arrival
- * counters the library keeps per stream (the first 1024 streams; beyond them, or
- * beyond 256 split rows, two launches with the same result).  The workspace's
- * contents on entry do not matter. */
+ * counters the library keeps per stream (the first 1024 streams; beyond them,
+ * beyond 256 split rows, or while the stream is being captured into a graph,
+ * two launches with the same result).  The workspace's contents on entry do
+ * not matter. */
 int mcke_launch_row_reduce_ws_f32(const float* x, float* out, int64_t rows, int64_t cols,
                                   int kind, int variant, float* workspace,
                                   size_t workspace_bytes, void* stream);

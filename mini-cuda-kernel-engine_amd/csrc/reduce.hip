@@ -58,12 +58,13 @@ constexpr int64_t kMaxSplit = 65535;
 // object loads).  A launch takes the block of kCountersPerBlock counters that
 // belongs to its stream (for the per-thread default stream: to that stream in
 // the calling thread), one counter per row.  Launches on one stream run one
-// after another -- and a captured graph keeps the order of the nodes captured
-// on one stream -- so two launches that run at the same time never share a
+// after another, so two launches that run at the same time never share a
 // counter.  Every counter is zero at rest: the workgroup that arrives last on a
-// row resets it.  Launches with more rows than a block holds, or on a stream
-// beyond the first kCounterBlocks seen, fall back to two launches (partials,
-// then a one-workgroup-per-row fold) and use no counter.
+// row resets it.  Launches with more rows than a block holds, on a stream
+// beyond the first kCounterBlocks seen, or captured into a graph (which may be
+// replayed on any stream, beside eager launches on the stream it was captured
+// from) fall back to two launches (partials, then a one-workgroup-per-row fold)
+// and use no counter.
 constexpr int kCounterBlocks = 1024;
 constexpr int kCountersPerBlock = 256;
 __device__ unsigned int g_row_arrivals[kCounterBlocks * kCountersPerBlock];
@@ -292,6 +293,17 @@ int64_t two_pass_split(int64_t rows, int64_t cols) {
   return s;
 }
 
+// True while `st` is being captured into a graph, or when its capture state
+// cannot be read (the launch itself then reports what is wrong with the stream).
+bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &status) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return status != hipStreamCaptureStatusNone;
+}
+
 template <class Op, bool MEAN>
 int launch_one_pass(const float* x, float* out, int64_t rows, int64_t cols, bool tree,
                     hipStream_t st) {
@@ -316,7 +328,7 @@ int launch_two_pass(const float* x, float* out, int64_t rows, int64_t cols, floa
   chunk = (chunk + 3) & ~static_cast<int64_t>(3);
   const bool vec = (cols % 4 == 0) && aligned(x, 16);
   int counter_base = -1;
-  if (split > 1 && rows <= kCountersPerBlock) {
+  if (split > 1 && rows <= kCountersPerBlock && !capturing(st)) {
     const int b = counter_block(st);
     if (b >= 0) counter_base = b * kCountersPerBlock;
   }

@@ -362,9 +362,10 @@ def test_16bit_gemm_node_feeds_f32_ops(G, orc, dt):
 
 
 def test_captured_split_reduce_replays(G, orc):
-    """kTwoPass nodes whose rows split over workgroups, so their one-launch fold
-    runs on the arrival counters of the stream each was captured on; two of them
-    on different streams of one captured graph.  Every replay, also after new
+    """kTwoPass nodes whose rows split over workgroups (captured, they take the
+    two-launch path, partials then fold, since a graph may be replayed on any
+    stream); two of them on different streams of one captured graph.  Every
+    replay, also after new
     inputs, matches the eager launch's bits and the double-accumulating CPU
     reduce (reference tests/reference.hpp:154-172)."""
     g = G.Graph()

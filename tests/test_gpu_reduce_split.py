@@ -12,7 +12,9 @@ accumulating CPU reduce (reference tests/reference.hpp:154-172; max bit-exact):
   do two host threads launching on the per-thread default stream;
 * once the stream table is full (a fresh process that has launched on 1024
   streams), a launch on a further stream falls back to two launches and still
-  gives the same result.
+  gives the same result;
+* a launch captured into a graph uses no stream's counters, so a replay on
+  another stream beside eager launches on the capture stream stays right.
 """
 from __future__ import annotations
 
@@ -194,3 +196,56 @@ def test_per_thread_default_stream_in_two_threads(gpu, orc):
         got = np.array([o.download(1)[0] for o in outs], np.float32)
         _check(orc, inputs[t], 1, n, 0, got[:1])
         assert np.all(got.view(np.uint32) == got.view(np.uint32)[0]), f"thread {t}"
+
+
+def test_graph_replayed_beside_its_capture_stream(gpu, orc):
+    """A split kTwoPass launch captured into a graph on stream S1 and replayed on
+    stream S2 while eager kTwoPass launches of the same shape run on S1.  A graph
+    may run on any stream, so a captured launch counts on no stream's counters
+    (it takes the two-launch path): every eager launch and the last replay give
+    the CPU result, and S1's counters are at rest afterwards (a further launch
+    on S1 is right too)."""
+    import ctypes as C
+
+    m = gpu
+    L = m.lib()
+    VP = C.c_void_p
+    for name, args in (("mcke_rt_stream_begin_capture", [VP]),
+                       ("mcke_rt_stream_end_capture", [VP, C.POINTER(VP)]),
+                       ("mcke_rt_graph_launch", [VP, VP]),
+                       ("mcke_rt_graph_destroy", [VP])):
+        getattr(L, name).restype = C.c_int
+        getattr(L, name).argtypes = args
+    D = m.DeviceBuffer
+    TP = m.ReduceVariant.kTwoPass
+    rows, cols = 2, 1 << 20                   # 128 workgroups per row
+    wsb = m.row_reduce_workspace_bytes(rows, cols, TP)
+    s1, s2 = m.Stream(), m.Stream()
+    exe = VP()
+    try:
+        xg = orc.fill_normal(rows * cols, 0xCA97)
+        dxg, outg, wsg = D.from_array(xg), D(rows * 4), D(wsb)
+        assert L.mcke_rt_stream_begin_capture(s1.handle) == 0
+        _launch(m, dxg, outg, rows, cols, 0, wsg, wsb, s1)
+        assert L.mcke_rt_stream_end_capture(s1.handle, C.byref(exe)) == 0 and exe.value
+        eager = []
+        for i in range(8):
+            x = orc.fill_normal(rows * cols, 0xE6E0 + i)
+            eager.append((x, D.from_array(x), D(rows * 4), D(wsb)))
+        for _x, dx, dout, ws in eager:
+            assert L.mcke_rt_graph_launch(exe, s2.handle) == 0
+            _launch(m, dx, dout, rows, cols, 0, ws, wsb, s1)
+        s1.synchronize()
+        s2.synchronize()
+        for x, _dx, dout, _ws in eager:
+            _check(orc, x, rows, cols, 0, dout.download(rows))
+        _check(orc, xg, rows, cols, 0, outg.download(rows))
+        x, dx, dout, ws = eager[0]
+        _launch(m, dx, dout, rows, cols, 1, ws, wsb, s1)
+        s1.synchronize()
+        _check(orc, x, rows, cols, 1, dout.download(rows))
+    finally:
+        if exe.value:
+            L.mcke_rt_graph_destroy(exe)
+        s1.close()
+        s2.close()
