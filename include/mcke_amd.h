@@ -136,6 +136,12 @@ int mcke_max_vector_width_f32(const void* p, int64_t cols);
  * partials), where this build's split depends on the shape (rows and cols). */
 size_t mcke_row_reduce_workspace_bytes(int64_t rows, int64_t cols, int variant);
 
+/* No counterpart in the reference: the number of kTwoPass counter blocks a
+ * launch on a stream not seen before could take now (unused blocks, plus blocks
+ * of streams destroyed through mcke_rt_stream_destroy whose work has completed).
+ * For callers that create and destroy many streams. */
+int mcke_reduce_counter_blocks_free(void);
+
 /* The frozen 7-argument launch_row_reduce_f32, kernels.hpp:204-207 /
  * reduce.cu:285-295: kTwoPass without a workspace is UNIMPLEMENTED. */
 int mcke_launch_row_reduce_f32(const float* x, float* out, int64_t rows, int64_t cols,
@@ -145,9 +151,10 @@ int mcke_launch_row_reduce_f32(const float* x, float* out, int64_t rows, int64_t
  * out[r] = sum / max / mean of row r (mean = sum / cols).  rows == 1 with
  * kTwoPass is the full-tensor reduction.  kTwoPass is one launch: the workgroup
  * that finishes a split row last folds the row's partials, counted on arrival
- * counters the library keeps per stream (the first 1024 streams; beyond them,
- * beyond 256 split rows, or while the stream is being captured into a graph,
- * two launches with the same result).  The workspace's contents on entry do
+ * counters the library keeps per stream (1024 blocks; a stream destroyed through
+ * mcke_rt_stream_destroy gives its block back once its work completes; with every
+ * block taken, beyond 256 split rows, or while the stream is being captured into
+ * a graph, two launches with the same result).  The workspace's contents on entry do
  * not matter. */
 int mcke_launch_row_reduce_ws_f32(const float* x, float* out, int64_t rows, int64_t cols,
                                   int kind, int variant, float* workspace,

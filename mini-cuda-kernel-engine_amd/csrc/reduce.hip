@@ -31,6 +31,7 @@
 #include <type_traits>
 #include <unordered_map>
 #include <utility>
+#include <vector>
 
 #include "common.hpp"
 #include "device_math.hpp"
@@ -60,8 +61,10 @@ constexpr int64_t kMaxSplit = 65535;
 // the calling thread), one counter per row.  Launches on one stream run one
 // after another, so two launches that run at the same time never share a
 // counter.  Every counter is zero at rest: the workgroup that arrives last on a
-// row resets it.  Launches with more rows than a block holds, on a stream
-// beyond the first kCounterBlocks seen, or captured into a graph (which may be
+// row resets it.  A stream destroyed through mcke_rt_stream_destroy gives its
+// block back once its queued work completes.  Launches with more rows than a
+// block holds, on a new stream while every block is taken, or captured into a
+// graph (which may be
 // replayed on any stream, beside eager launches on the stream it was captured
 // from) fall back to two launches (partials, then a one-workgroup-per-row fold)
 // and use no counter.
@@ -258,27 +261,61 @@ __global__ __launch_bounds__(kSplitThreads) void row_reduce_fold_kernel(
   if (threadIdx.x == 0) out[r] = t;
 }
 
-// The counter block of `stream`, or -1 when the stream table is full.  The
-// per-thread default stream is one handle value that names a different stream
-// in each host thread, so it is keyed by the calling thread as well; every
-// other handle (the legacy null stream included) names one stream whatever
-// thread launches on it.
-int counter_block(hipStream_t stream) {
-  using Key = std::pair<hipStream_t, std::thread::id>;
-  struct KeyHash {
-    std::size_t operator()(const Key& k) const {
-      return std::hash<const void*>()(k.first) ^ (std::hash<std::thread::id>()(k.second) << 1);
+// The stream table: which counter block each stream has, and the blocks of
+// destroyed streams.  The per-thread default stream is one handle value that
+// names a different stream in each host thread, so it is keyed by the calling
+// thread as well; every other handle (the legacy null stream included) names
+// one stream whatever thread launches on it.
+using StreamKey = std::pair<hipStream_t, std::thread::id>;
+struct StreamKeyHash {
+  std::size_t operator()(const StreamKey& k) const {
+    return std::hash<const void*>()(k.first) ^ (std::hash<std::thread::id>()(k.second) << 1);
+  }
+};
+struct RetiredBlock {
+  int block;
+  hipEvent_t done;   // recorded after the destroyed stream's last launch
+};
+struct CounterTable {
+  std::mutex mu;
+  std::unordered_map<StreamKey, int, StreamKeyHash> blocks;
+  std::vector<RetiredBlock> retired;
+  int issued = 0;    // blocks [0, issued) have been handed out at least once
+};
+
+// Never destroyed: streams may be retired from static destructors of callers.
+CounterTable& counter_table() {
+  static CounterTable* t = new CounterTable;
+  return *t;
+}
+
+// A retired block whose stream's work has completed, or -1.  A block is handed
+// out again only then, so a launch on its new stream never shares a counter
+// with a launch still running on the destroyed one.
+int take_retired(CounterTable& t) {
+  for (std::size_t i = 0; i < t.retired.size(); ++i) {
+    const hipError_t q = hipEventQuery(t.retired[i].done);
+    if (q == hipSuccess) {
+      const int b = t.retired[i].block;
+      (void)hipEventDestroy(t.retired[i].done);
+      t.retired.erase(t.retired.begin() + static_cast<std::ptrdiff_t>(i));
+      return b;
     }
-  };
-  static std::mutex mu;
-  static std::unordered_map<Key, int, KeyHash> blocks;
-  const Key key{stream, stream == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id()};
-  std::lock_guard<std::mutex> lock(mu);
-  const auto it = blocks.find(key);
-  if (it != blocks.end()) return it->second;
-  if (blocks.size() >= static_cast<std::size_t>(kCounterBlocks)) return -1;
-  const int b = static_cast<int>(blocks.size());
-  blocks.emplace(key, b);
+    (void)hipGetLastError();   // not ready yet: no error of the caller's
+  }
+  return -1;
+}
+
+// The counter block of `stream`, or -1 when every block is taken.
+int counter_block(hipStream_t stream) {
+  CounterTable& t = counter_table();
+  const StreamKey key{stream, stream == hipStreamPerThread ? std::this_thread::get_id()
+                                                           : std::thread::id()};
+  std::lock_guard<std::mutex> lock(t.mu);
+  const auto it = t.blocks.find(key);
+  if (it != t.blocks.end()) return it->second;
+  const int b = t.issued < kCounterBlocks ? t.issued++ : take_retired(t);
+  if (b >= 0) t.blocks.emplace(key, b);
   return b;
 }
 
@@ -350,11 +387,54 @@ int launch_two_pass(const float* x, float* out, int64_t rows, int64_t cols, floa
 }
 
 }  // namespace
+
+void retire_counter_blocks(hipStream_t stream) {
+  if (!stream || stream == hipStreamPerThread) return;   // never destroyed
+  CounterTable& t = counter_table();
+  std::lock_guard<std::mutex> lock(t.mu);
+  for (auto it = t.blocks.begin(); it != t.blocks.end();) {
+    if (it->first.first != stream) {
+      ++it;
+      continue;
+    }
+    // The event must belong to the stream's device.
+    int cur = -1, dev = -1;
+    hipEvent_t done = nullptr;
+    const bool switched = hipGetDevice(&cur) == hipSuccess &&
+                          hipStreamGetDevice(stream, &dev) == hipSuccess && dev != cur &&
+                          hipSetDevice(dev) == hipSuccess;
+    if (hipEventCreateWithFlags(&done, hipEventDisableTiming) == hipSuccess &&
+        hipEventRecord(done, stream) == hipSuccess) {
+      t.retired.push_back({it->second, done});
+    } else {
+      // The block cannot be shown idle later: it is never handed out again.
+      if (done) (void)hipEventDestroy(done);
+      (void)hipGetLastError();
+    }
+    if (switched) (void)hipSetDevice(cur);
+    it = t.blocks.erase(it);
+  }
+}
+
+int counter_blocks_free() {
+  CounterTable& t = counter_table();
+  std::lock_guard<std::mutex> lock(t.mu);
+  int idle = 0;
+  for (const RetiredBlock& r : t.retired) {
+    const hipError_t q = hipEventQuery(r.done);
+    if (q == hipSuccess) ++idle;
+    else (void)hipGetLastError();
+  }
+  return (kCounterBlocks - t.issued) + idle;
+}
+
 }  // namespace mcke_amd
 
 using namespace mcke_amd;
 
 extern "C" {
+
+int mcke_reduce_counter_blocks_free(void) { return counter_blocks_free(); }
 
 size_t mcke_row_reduce_workspace_bytes(int64_t rows, int64_t cols, int variant) {
   if (variant != MCKE_REDUCE_TWO_PASS || rows <= 0) return 0;

@@ -125,6 +125,7 @@ int mcke_rt_stream_create(void** out_stream) {
 
 int mcke_rt_stream_destroy(void* stream) {
   if (!stream) return ok();
+  retire_counter_blocks(static_cast<hipStream_t>(stream));
   MCKE_HIP_TRY(hipStreamDestroy(static_cast<hipStream_t>(stream)));
   return ok();
 }

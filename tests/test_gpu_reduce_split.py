@@ -13,6 +13,8 @@ accumulating CPU reduce (reference tests/reference.hpp:154-172; max bit-exact):
 * once the stream table is full (a fresh process that has launched on 1024
   streams), a launch on a further stream falls back to two launches and still
   gives the same result;
+* a stream destroyed through the library gives its counter block back once
+  its work has completed, so streams created later still get one;
 * a launch captured into a graph uses no stream's counters, so a replay on
   another stream beside eager launches on the capture stream stays right.
 """
@@ -148,6 +150,7 @@ bad = [i for i in range(len(got)) if got[i].view(np.uint32) != got[0].view(np.ui
 assert not bad, f"streams {{bad[:5]}} differ: {{got[bad[:5]]}} vs {{got[0]}}"
 r = oracle.compare(got[:1], want, 1e-5, 5e-5 * 2.0)
 assert r.ok, str(r)
+assert m.lib().mcke_reduce_counter_blocks_free() == 0
 print("fallback-ok", len(got))
 """
 
@@ -159,6 +162,63 @@ def test_stream_table_full_falls_back(gpu):
     p = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
     assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
     assert "fallback-ok 1025" in p.stdout
+
+
+_RECYCLE_SCRIPT = r"""
+import sys
+sys.path.insert(0, {root!r})
+import numpy as np
+from __graft_entry__ import load_package
+import oracle
+m = load_package()
+m.require_gpu()
+D = m.DeviceBuffer
+TP = m.ReduceVariant.kTwoPass
+free = m.lib().mcke_reduce_counter_blocks_free
+cols = 8192                      # rows == 1 splits in two
+x = oracle.fill_normal(cols, 0x2EC1)
+dx = D.from_array(x)
+wsb = m.row_reduce_workspace_bytes(1, cols, TP)
+assert free() == 1024, free()
+outs, wss = [], []
+def launch(st):
+    o, ws = D(4), D(wsb)
+    m.launch_row_reduce_f32(dx, o, 1, cols, 0, TP, ws, wsb, st).throw_if_error()
+    outs.append(o)
+    wss.append(ws)
+for i in range(1024):            # each stream destroyed while its launch may still run
+    st = m.Stream()
+    launch(st)
+    st.close()
+m.device_synchronize()
+assert free() == 1024, free()    # every block came back once its work completed
+live = [m.Stream() for _ in range(100)]
+for st in live:                  # no unused block left: these take retired ones
+    launch(st)
+assert free() == 924, free()
+for st in live:
+    st.close()
+m.device_synchronize()
+assert free() == 1024, free()
+want = oracle.row_reduce(x, 1, cols, 0)
+got = np.array([o.download(1)[0] for o in outs], np.float32)
+bad = [i for i in range(len(got)) if got[i].view(np.uint32) != got[0].view(np.uint32)]
+assert not bad, f"launches {{bad[:5]}} differ: {{got[bad[:5]]}} vs {{got[0]}}"
+r = oracle.compare(got[:1], want, 1e-5, 5e-5 * 2.0)
+assert r.ok, str(r)
+print("recycle-ok", len(got))
+"""
+
+
+def test_destroyed_streams_give_their_blocks_back(gpu):
+    """In a fresh process: 1024 streams each launched on and destroyed without a
+    wait, then 100 more.  A destroyed stream's counter block is handed out again
+    once its work has completed, so the later streams still take the one-launch
+    path, and every result has the same bits and matches the CPU sum."""
+    code = _RECYCLE_SCRIPT.format(root=ROOT)
+    p = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    assert "recycle-ok 1124" in p.stdout
 
 
 def test_per_thread_default_stream_in_two_threads(gpu, orc):
