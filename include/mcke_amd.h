@@ -136,12 +136,6 @@ int mcke_max_vector_width_f32(const void* p, int64_t cols);
  * partials), where this build's split depends on the shape (rows and cols). */
 size_t mcke_row_reduce_workspace_bytes(int64_t rows, int64_t cols, int variant);
 
-/* No counterpart in the reference: the number of kTwoPass counter blocks a
- * launch on a stream not seen before could take now (unused blocks, plus blocks
- * of streams destroyed through mcke_rt_stream_destroy whose work has completed).
- * For callers that create and destroy many streams. */
-int mcke_reduce_counter_blocks_free(void);
-
 /* The frozen 7-argument launch_row_reduce_f32, kernels.hpp:204-207 /
  * reduce.cu:285-295: kTwoPass without a workspace is UNIMPLEMENTED. */
 int mcke_launch_row_reduce_f32(const float* x, float* out, int64_t rows, int64_t cols,
@@ -149,13 +143,11 @@ int mcke_launch_row_reduce_f32(const float* x, float* out, int64_t rows, int64_t
 
 /* The 9-argument launch_row_reduce_f32, kernels.hpp:209-213 / reduce.cu:224-280.
  * out[r] = sum / max / mean of row r (mean = sum / cols).  rows == 1 with
- * kTwoPass is the full-tensor reduction.  kTwoPass is one launch: the workgroup
- * that finishes a split row last folds the row's partials, counted on arrival
- * counters the library keeps per stream (1024 blocks; a stream destroyed through
- * mcke_rt_stream_destroy gives its block back once its work completes; with every
- * block taken, beyond 256 split rows, or while the stream is being captured into
- * a graph, two launches with the same result).  The workspace's contents on entry do
- * not matter. */
+ * kTwoPass is the full-tensor reduction.  When there are too few rows to fill
+ * the part, kTwoPass splits each long row into column chunks whose partials go
+ * to the workspace, and a second launch folds each row's partials in a fixed
+ * order; rows that need no split take one launch.  The launcher keeps no state
+ * between calls, and the workspace's contents on entry do not matter. */
 int mcke_launch_row_reduce_ws_f32(const float* x, float* out, int64_t rows, int64_t cols,
                                   int kind, int variant, float* workspace,
                                   size_t workspace_bytes, void* stream);
@@ -279,6 +271,9 @@ int mcke_rt_host_alloc(void** out_ptr, size_t bytes); /* pinned host memory */
 int mcke_rt_host_free(void* ptr);
 /* kind: 0 host->device, 1 device->host, 2 device->device, 3 default (unified VA). */
 int mcke_rt_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream);
+/* Refused (INVALID_ARGUMENT) while `stream` is being captured into a graph: a
+ * captured memset node is not replayed reliably on this stack; capture
+ * mcke_fill_u32_async instead. */
 int mcke_rt_memset_async(void* dst, int value, size_t bytes, void* stream);
 /* No reference counterpart: fills `count` 32-bit words with `value` using a
  * kernel (usable under graph capture, unlike a memset node).  Used by the graph

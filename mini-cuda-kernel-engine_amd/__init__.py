@@ -197,7 +197,6 @@ def lib() -> C.CDLL:
         "mcke_rt_get_device": (C.c_int, [C.POINTER(C.c_int)]),
         "mcke_rt_query_device": (C.c_int, [C.c_int, C.POINTER(DeviceInfo)]),
         "mcke_rt_device_synchronize": (C.c_int, []),
-        "mcke_reduce_counter_blocks_free": (C.c_int, []),
         "mcke_rt_stream_create": (C.c_int, [C.POINTER(_VP)]),
         "mcke_rt_stream_destroy": (C.c_int, [_VP]),
         "mcke_rt_stream_synchronize": (C.c_int, [_VP]),

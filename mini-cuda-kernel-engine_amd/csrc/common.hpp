@@ -42,11 +42,4 @@ inline bool aligned(const void* p, std::size_t bytes) {
 // Wavefront width on CDNA.  Kernels are written for 64 lanes.
 constexpr int kWave = 64;
 
-// kTwoPass arrival counters (reduce.hip): called before `stream` is destroyed.
-// Its counter block is handed out again once the work queued on it so far has
-// completed; the destroy itself does not wait.
-void retire_counter_blocks(hipStream_t stream);
-// Counter blocks a kTwoPass launch on a stream not seen before could take now.
-int counter_blocks_free();
-
 }  // namespace mcke_amd

@@ -10,13 +10,14 @@
 //   kWarpShuffle one workgroup per row; wave64 butterfly, then one LDS stage
 //                across the 4 waves (1 barrier);
 //   kTwoPass     (rows x split) workgroups reduce column chunks of a row to
-//                partials in the caller's workspace; the workgroup that
-//                finishes a row last (an arrival counter per row) folds that
-//                row's partials in a fixed order and writes out[r], all in one
-//                launch.  With rows == 1 this is the full-tensor reduction.
-// Every variant is deterministic: no value is combined atomically (the only
-// atomic is kTwoPass's arrival count), so the same input gives the same bits on
-// every run.
+//                partials in the caller's workspace, then one workgroup per
+//                row folds that row's partials in a fixed order (a second
+//                launch, as reduce.cu:180-206).  Rows that need no split are
+//                written out by the first launch, which is then the only one.
+//                With rows == 1 this is the full-tensor reduction.
+// Every variant is deterministic (nothing is combined atomically) and keeps no
+// state between launches: the same input gives the same bits on every run, on
+// any stream.
 //
 // The row sweep: 256 lanes walk the row in 16-byte (float4) steps when the row
 // starts are 16-byte aligned, four loads in flight per lane before any add.
@@ -25,13 +26,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
-#include <mutex>
 #include <string>
-#include <thread>
 #include <type_traits>
-#include <unordered_map>
-#include <utility>
-#include <vector>
 
 #include "common.hpp"
 #include "device_math.hpp"
@@ -43,34 +39,16 @@ constexpr int kThreads = 256;
 constexpr int kLoadUnroll = 4;      // loads in flight per lane, one-pass kernels
 // kTwoPass sizing: one 512-lane workgroup per CU on a 256-CU part, each lane
 // keeping 4 float4 loads in flight.  Measured on the full-tensor sum of 2^26
-// floats (one launch, fold by the last arrival), workgroups x lanes x loads:
-// 256 x 512 x 4 40.6 us, 256 x 256 x 8 40.9 us, 256 x 1024 x 2 40.9 us,
-// 256 x 1024 x 4 42.9 us, 512 x 256 x 8 42.5 us, 1024 x 256 x 8 44.9 us,
-// 2048 x 256 x 8 50.3 us -- each workgroup ends with a round trip (its partial's
-// store, then the arrival count) during which its slot issues no loads, so few,
+// floats, workgroups x lanes x loads: 256 x 512 x 4 40.6 us, 256 x 256 x 8
+// 40.9 us, 256 x 1024 x 2 40.9 us, 256 x 1024 x 4 42.9 us, 512 x 256 x 8
+// 42.5 us, 1024 x 256 x 8 44.9 us, 2048 x 256 x 8 50.3 us -- each workgroup
+// ends with its partial's store, during which its slot issues no loads, so few,
 // wide workgroups win.
 constexpr int kSplitThreads = 512;
 constexpr int kPass1Unroll = 4;
 constexpr int64_t kTargetBlocks = 256;
 constexpr int64_t kMinColsPerBlock = 4096;
 constexpr int64_t kMaxSplit = 65535;
-
-// Arrival counters of kTwoPass rows, owned by the library (zero when the code
-// object loads).  A launch takes the block of kCountersPerBlock counters that
-// belongs to its stream (for the per-thread default stream: to that stream in
-// the calling thread), one counter per row.  Launches on one stream run one
-// after another, so two launches that run at the same time never share a
-// counter.  Every counter is zero at rest: the workgroup that arrives last on a
-// row resets it.  A stream destroyed through mcke_rt_stream_destroy gives its
-// block back once its queued work completes.  Launches with more rows than a
-// block holds, on a new stream while every block is taken, or captured into a
-// graph (which may be
-// replayed on any stream, beside eager launches on the stream it was captured
-// from) fall back to two launches (partials, then a one-workgroup-per-row fold)
-// and use no counter.
-constexpr int kCounterBlocks = 1024;
-constexpr int kCountersPerBlock = 256;
-__device__ unsigned int g_row_arrivals[kCounterBlocks * kCountersPerBlock];
 
 struct SumOp {
   static __device__ __forceinline__ float identity() { return 0.0f; }
@@ -164,24 +142,17 @@ __global__ __launch_bounds__(kThreads) void row_reduce_kernel(const float* __res
 }
 
 // Folds the `split` partials p[0, split) of one row in a fixed order (lane-
-// strided, then a wave64 butterfly, then the 4 waves in order); the result is
+// strided, then a wave64 butterfly, then the waves in order); the result is
 // valid in thread 0.  Sums are carried in double: the partials are few and this
-// stage should not add error on top of the first.  COHERENT reads the partials
-// with device-scope loads (they were written by other workgroups of the same
-// launch, possibly on another XCD, whose L2 this one does not share).
-template <class Op, bool MEAN, bool COHERENT, int NT = kThreads>
-__device__ __forceinline__ float fold_partials(const float* p, int64_t split, int64_t cols) {
-  auto get = [&](int64_t i) -> float {
-    if constexpr (COHERENT)
-      return __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-      return p[i];
-  };
+// stage should not add error on top of the first.
+template <class Op, bool MEAN, int NT>
+__device__ __forceinline__ float fold_partials(const float* __restrict__ p, int64_t split,
+                                               int64_t cols) {
   const int w = threadIdx.x / kWave;
   if constexpr (std::is_same_v<Op, SumOp>) {
     __shared__ double part[NT / kWave];
     double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < split; i += NT) acc += static_cast<double>(get(i));
+    for (int64_t i = threadIdx.x; i < split; i += NT) acc += static_cast<double>(p[i]);
 #pragma unroll
     for (int m = kWave / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
     if ((threadIdx.x % kWave) == 0) part[w] = acc;
@@ -192,30 +163,19 @@ __device__ __forceinline__ float fold_partials(const float* p, int64_t split, in
     return static_cast<float>(MEAN ? t / static_cast<double>(cols) : t);
   } else {
     float acc = Op::identity();
-    for (int64_t i = threadIdx.x; i < split; i += NT) acc = Op::apply(acc, get(i));
+    for (int64_t i = threadIdx.x; i < split; i += NT) acc = Op::apply(acc, p[i]);
     return block_combine_shfl<Op, NT>(acc);
   }
 }
 
-// kTwoPass, workgroup (s, r): reduces columns [s*chunk, min(cols, (s+1)*chunk))
-// of row r.  With split == 1 the workgroup owns the row and writes out[r].
-// Otherwise it stores its partial to ws[r*split + s]; with a counter block
-// (counter_base >= 0) it then counts its arrival on row r, and the workgroup
-// that arrives last folds the row's partials into out[r].  Without a counter
-// block, out[] is left to row_reduce_fold_kernel.
-//
-// Ordering.  The partial is stored at device scope (a write-through store that
-// bypasses this XCD's L2), and the workgroup waits for that store to complete
-// before it counts its arrival, so every partial counted before the last
-// arrival is already at the device's point of coherence; the fold reads them
-// with device-scope loads that bypass the L2 as well.  The counter add itself is
-// relaxed: an acquire-release add here costs an L2 writeback and invalidate per
-// workgroup (measured: the launch takes 49 us instead of 41 us at 256
-// workgroups), and only the partial needs publishing.
+// kTwoPass, first launch, workgroup (s, r): reduces columns
+// [s*chunk, min(cols, (s+1)*chunk)) of row r.  With split == 1 the workgroup owns
+// the row and writes out[r]; otherwise it stores its partial to
+// part[r*split + s] for row_reduce_fold_kernel.
 template <class Op, bool VEC, bool MEAN>
 __global__ __launch_bounds__(kSplitThreads) void row_reduce_split_kernel(
-    const float* __restrict__ x, float* __restrict__ ws, float* __restrict__ out, int64_t cols,
-    int64_t chunk, int64_t split, int counter_base) {
+    const float* __restrict__ x, float* __restrict__ part, float* __restrict__ out, int64_t cols,
+    int64_t chunk, int64_t split) {
   const int64_t s = blockIdx.x;
   const int64_t r = blockIdx.y;
   const int64_t begin = s * chunk;
@@ -224,99 +184,20 @@ __global__ __launch_bounds__(kSplitThreads) void row_reduce_split_kernel(
   float v = Op::identity();
   if (begin < end) v = thread_partial<Op, VEC, kPass1Unroll, kSplitThreads>(x + r * cols, begin, end);
   v = block_combine_shfl<Op, kSplitThreads>(v);
-  if (split == 1) {
-    if (threadIdx.x == 0) out[r] = MEAN ? v / static_cast<float>(cols) : v;
-    return;
-  }
-  __shared__ int last;
-  if (threadIdx.x == 0) {
-    __hip_atomic_store(ws + r * split + s, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    int is_last = 0;
-    if (counter_base >= 0) {
-      unsigned int* cnt = g_row_arrivals + counter_base + r;
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the partial's store has completed
-      const unsigned int prev =
-          __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      is_last = (prev == static_cast<unsigned int>(split - 1));
-      if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      // Every arrival of this row has been counted: rest the counter at zero.
-      if (is_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    last = is_last;
-  }
-  __syncthreads();
-  if (!last) return;
-  const float t = fold_partials<Op, MEAN, true, kSplitThreads>(ws + r * split, split, cols);
-  if (threadIdx.x == 0) out[r] = t;
+  if (threadIdx.x != 0) return;
+  if (split == 1)
+    out[r] = MEAN ? v / static_cast<float>(cols) : v;
+  else
+    part[r * split + s] = v;
 }
 
-// The fold as a launch of its own (one workgroup per row), for kTwoPass launches
-// that have no counter block.  Same lane count and order as the last arrival's
-// fold, so both paths give the same bits.
+// kTwoPass, second launch: one workgroup per row folds that row's partials.
 template <class Op, bool MEAN>
 __global__ __launch_bounds__(kSplitThreads) void row_reduce_fold_kernel(
-    const float* __restrict__ ws, float* __restrict__ out, int64_t split, int64_t cols) {
+    const float* __restrict__ part, float* __restrict__ out, int64_t split, int64_t cols) {
   const int64_t r = blockIdx.x;
-  const float t = fold_partials<Op, MEAN, false, kSplitThreads>(ws + r * split, split, cols);
+  const float t = fold_partials<Op, MEAN, kSplitThreads>(part + r * split, split, cols);
   if (threadIdx.x == 0) out[r] = t;
-}
-
-// The stream table: which counter block each stream has, and the blocks of
-// destroyed streams.  The per-thread default stream is one handle value that
-// names a different stream in each host thread, so it is keyed by the calling
-// thread as well; every other handle (the legacy null stream included) names
-// one stream whatever thread launches on it.
-using StreamKey = std::pair<hipStream_t, std::thread::id>;
-struct StreamKeyHash {
-  std::size_t operator()(const StreamKey& k) const {
-    return std::hash<const void*>()(k.first) ^ (std::hash<std::thread::id>()(k.second) << 1);
-  }
-};
-struct RetiredBlock {
-  int block;
-  hipEvent_t done;   // recorded after the destroyed stream's last launch
-};
-struct CounterTable {
-  std::mutex mu;
-  std::unordered_map<StreamKey, int, StreamKeyHash> blocks;
-  std::vector<RetiredBlock> retired;
-  int issued = 0;    // blocks [0, issued) have been handed out at least once
-};
-
-// Never destroyed: streams may be retired from static destructors of callers.
-CounterTable& counter_table() {
-  static CounterTable* t = new CounterTable;
-  return *t;
-}
-
-// A retired block whose stream's work has completed, or -1.  A block is handed
-// out again only then, so a launch on its new stream never shares a counter
-// with a launch still running on the destroyed one.
-int take_retired(CounterTable& t) {
-  for (std::size_t i = 0; i < t.retired.size(); ++i) {
-    const hipError_t q = hipEventQuery(t.retired[i].done);
-    if (q == hipSuccess) {
-      const int b = t.retired[i].block;
-      (void)hipEventDestroy(t.retired[i].done);
-      t.retired.erase(t.retired.begin() + static_cast<std::ptrdiff_t>(i));
-      return b;
-    }
-    (void)hipGetLastError();   // not ready yet: no error of the caller's
-  }
-  return -1;
-}
-
-// The counter block of `stream`, or -1 when every block is taken.
-int counter_block(hipStream_t stream) {
-  CounterTable& t = counter_table();
-  const StreamKey key{stream, stream == hipStreamPerThread ? std::this_thread::get_id()
-                                                           : std::thread::id()};
-  std::lock_guard<std::mutex> lock(t.mu);
-  const auto it = t.blocks.find(key);
-  if (it != t.blocks.end()) return it->second;
-  const int b = t.issued < kCounterBlocks ? t.issued++ : take_retired(t);
-  if (b >= 0) t.blocks.emplace(key, b);
-  return b;
 }
 
 int64_t two_pass_split(int64_t rows, int64_t cols) {
@@ -328,17 +209,6 @@ int64_t two_pass_split(int64_t rows, int64_t cols) {
   if (s > kMaxSplit) s = kMaxSplit;
   if (s < 1) s = 1;
   return s;
-}
-
-// True while `st` is being captured into a graph, or when its capture state
-// cannot be read (the launch itself then reports what is wrong with the stream).
-bool capturing(hipStream_t st) {
-  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &status) != hipSuccess) {
-    (void)hipGetLastError();
-    return true;
-  }
-  return status != hipStreamCaptureStatusNone;
 }
 
 template <class Op, bool MEAN>
@@ -356,85 +226,47 @@ int launch_one_pass(const float* x, float* out, int64_t rows, int64_t cols, bool
   return ok();
 }
 
+// `part` holds at least rows * two_pass_split(rows, cols) floats; it is written
+// before it is read, so its contents on entry do not matter.
 template <class Op, bool MEAN>
-int launch_two_pass(const float* x, float* out, int64_t rows, int64_t cols, float* ws,
+int launch_two_pass(const float* x, float* out, int64_t rows, int64_t cols, float* part,
                     hipStream_t st) {
   const int64_t split = two_pass_split(rows, cols);
   // chunk is a multiple of 4 so each chunk keeps the row's 16-byte alignment.
   int64_t chunk = (cols + split - 1) / split;
   chunk = (chunk + 3) & ~static_cast<int64_t>(3);
   const bool vec = (cols % 4 == 0) && aligned(x, 16);
-  int counter_base = -1;
-  if (split > 1 && rows <= kCountersPerBlock && !capturing(st)) {
-    const int b = counter_block(st);
-    if (b >= 0) counter_base = b * kCountersPerBlock;
-  }
   const dim3 g1(static_cast<unsigned>(split), static_cast<unsigned>(rows), 1u);
   if (vec)
-    row_reduce_split_kernel<Op, true, MEAN><<<g1, kSplitThreads, 0, st>>>(x, ws, out, cols, chunk,
-                                                                          split, counter_base);
+    row_reduce_split_kernel<Op, true, MEAN><<<g1, kSplitThreads, 0, st>>>(x, part, out, cols,
+                                                                          chunk, split);
   else
-    row_reduce_split_kernel<Op, false, MEAN><<<g1, kSplitThreads, 0, st>>>(x, ws, out, cols,
-                                                                           chunk, split,
-                                                                           counter_base);
+    row_reduce_split_kernel<Op, false, MEAN><<<g1, kSplitThreads, 0, st>>>(x, part, out, cols,
+                                                                           chunk, split);
   MCKE_LAUNCH_CHECK("row_reduce_split_kernel");
-  if (split > 1 && counter_base < 0) {
+  if (split > 1) {
     row_reduce_fold_kernel<Op, MEAN><<<static_cast<unsigned>(rows), kSplitThreads, 0, st>>>(
-        ws, out, split, cols);
+        part, out, split, cols);
     MCKE_LAUNCH_CHECK("row_reduce_fold_kernel");
   }
   return ok();
 }
 
+int dispatch_two_pass(const float* x, float* out, int64_t rows, int64_t cols, int kind,
+                      float* part, hipStream_t st) {
+  switch (kind) {
+    case MCKE_REDUCE_SUM: return launch_two_pass<SumOp, false>(x, out, rows, cols, part, st);
+    case MCKE_REDUCE_MEAN: return launch_two_pass<SumOp, true>(x, out, rows, cols, part, st);
+    default: return launch_two_pass<MaxOp, false>(x, out, rows, cols, part, st);
+  }
+}
+
 }  // namespace
-
-void retire_counter_blocks(hipStream_t stream) {
-  if (!stream || stream == hipStreamPerThread) return;   // never destroyed
-  CounterTable& t = counter_table();
-  std::lock_guard<std::mutex> lock(t.mu);
-  for (auto it = t.blocks.begin(); it != t.blocks.end();) {
-    if (it->first.first != stream) {
-      ++it;
-      continue;
-    }
-    // The event must belong to the stream's device.
-    int cur = -1, dev = -1;
-    hipEvent_t done = nullptr;
-    const bool switched = hipGetDevice(&cur) == hipSuccess &&
-                          hipStreamGetDevice(stream, &dev) == hipSuccess && dev != cur &&
-                          hipSetDevice(dev) == hipSuccess;
-    if (hipEventCreateWithFlags(&done, hipEventDisableTiming) == hipSuccess &&
-        hipEventRecord(done, stream) == hipSuccess) {
-      t.retired.push_back({it->second, done});
-    } else {
-      // The block cannot be shown idle later: it is never handed out again.
-      if (done) (void)hipEventDestroy(done);
-      (void)hipGetLastError();
-    }
-    if (switched) (void)hipSetDevice(cur);
-    it = t.blocks.erase(it);
-  }
-}
-
-int counter_blocks_free() {
-  CounterTable& t = counter_table();
-  std::lock_guard<std::mutex> lock(t.mu);
-  int idle = 0;
-  for (const RetiredBlock& r : t.retired) {
-    const hipError_t q = hipEventQuery(r.done);
-    if (q == hipSuccess) ++idle;
-    else (void)hipGetLastError();
-  }
-  return (kCounterBlocks - t.issued) + idle;
-}
-
 }  // namespace mcke_amd
 
 using namespace mcke_amd;
 
 extern "C" {
-
-int mcke_reduce_counter_blocks_free(void) { return counter_blocks_free(); }
 
 size_t mcke_row_reduce_workspace_bytes(int64_t rows, int64_t cols, int variant) {
   if (variant != MCKE_REDUCE_TWO_PASS || rows <= 0) return 0;
@@ -460,11 +292,7 @@ int mcke_launch_row_reduce_ws_f32(const float* x, float* out, int64_t rows, int6
                      " bytes of workspace (got " + std::to_string(workspace_bytes) +
                      "); query row_reduce_workspace_bytes() first");
     if (!aligned(workspace, 4)) return invalid("launch_row_reduce_f32: workspace not aligned");
-    switch (kind) {
-      case MCKE_REDUCE_SUM: return launch_two_pass<SumOp, false>(x, out, rows, cols, workspace, st);
-      case MCKE_REDUCE_MEAN: return launch_two_pass<SumOp, true>(x, out, rows, cols, workspace, st);
-      default: return launch_two_pass<MaxOp, false>(x, out, rows, cols, workspace, st);
-    }
+    return dispatch_two_pass(x, out, rows, cols, kind, workspace, st);
   }
 
   if (rows > 2147483647LL)

@@ -125,7 +125,6 @@ int mcke_rt_stream_create(void** out_stream) {
 
 int mcke_rt_stream_destroy(void* stream) {
   if (!stream) return ok();
-  retire_counter_blocks(static_cast<hipStream_t>(stream));
   MCKE_HIP_TRY(hipStreamDestroy(static_cast<hipStream_t>(stream)));
   return ok();
 }
@@ -378,7 +377,15 @@ int mcke_rt_memcpy_async(void* dst, const void* src, size_t bytes, int kind, voi
 int mcke_rt_memset_async(void* dst, int value, size_t bytes, void* stream) {
   if (bytes == 0) return ok();
   if (!dst) return invalid("mcke_rt_memset_async: null pointer");
-  MCKE_HIP_TRY(hipMemsetAsync(dst, value, bytes, static_cast<hipStream_t>(stream)));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  // A memset recorded into a graph has given wrong results on replays after the
+  // first on this stack; a fill kernel is the capturable way to clear memory.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  MCKE_HIP_TRY(hipStreamIsCapturing(st, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return invalid("mcke_rt_memset_async: the stream is being captured into a graph; "
+                   "use mcke_fill_u32_async, which records a kernel node");
+  MCKE_HIP_TRY(hipMemsetAsync(dst, value, bytes, st));
   return ok();
 }
 
