@@ -90,6 +90,7 @@ class Op:
         self.launches = 0
         self.single_ms: list[float] = []
         self.verify = None       # callable(oracle) -> dict, run in the CPU leg
+        self.cpu_ref = None      # callable(ref) -> output: the CPU reference on this op's input
         self.parity = None
         self.copy_peak = None    # measured 1R+1W ceiling (GB/s), when measured
 
@@ -205,6 +206,7 @@ def build_ops(m, stream, only=None):
                             "max_rel_err": r.max_rel_err,
                             "check": f"every row, rel 1e-5 + abs {floor:.3g}"}
                 ops[-1].verify = verify_reduce
+                ops[-1].cpu_ref = lambda ref, kind=kind: ref.row_reduce(hx, R, C_, int(kind))
     N26 = 1 << 26
     if want("full_sum"):
         log("generating full-sum input (2^26 U[0,1))")
@@ -226,6 +228,7 @@ def build_ops(m, stream, only=None):
             return {"ok": rel <= 1e-5, "max_rel_err": rel, "got": got, "want": want_,
                     "check": "rel 1e-5 against the double-accumulating CPU sum"}
         ops[-1].verify = verify_full
+        ops[-1].cpu_ref = lambda ref: ref.row_reduce(hxs, 1, N26, 0)
 
     # --- softmax -----------------------------------------------
     rows = 32768
@@ -247,13 +250,15 @@ def build_ops(m, stream, only=None):
 
         def verify_softmax(orc, x=x, dy=dy, cols=cols):
             got = dy[0].download(rows * cols)
-            r = orc.compare(got, orc.row_softmax(x, rows, cols), 1e-5, 1e-6)
+            r = orc.compare(got, orc.row_softmax(x, rows, cols), 0.0, 1e-6)
             sums = got.reshape(rows, cols).astype(np.float64).sum(axis=1)
             dev = float(np.max(np.abs(sums - 1.0)))
             return {"ok": bool(r.ok) and dev <= 1e-5, "max_abs_err": r.max_abs_err,
                     "max_row_sum_dev": dev,
-                    "check": "every element abs 1e-6 / rel 1e-5; every row sum within 1e-5"}
+                    "check": "every element within abs 1e-6 (BASELINE configs[2]); every row "
+                             "sum within 1e-5"}
         ops[-1].verify = verify_softmax
+        ops[-1].cpu_ref = lambda ref, x=x, cols=cols: ref.row_softmax(x, rows, cols)
 
     # --- bias + GELU(tanh) -------------------------------------
     for (br, bc) in ((16384, 4096), (4096, 1024)):
@@ -276,6 +281,8 @@ def build_ops(m, stream, only=None):
             return {"ok": bool(r.ok), "max_abs_err": r.max_abs_err, "max_rel_err": r.max_rel_err,
                     "check": "every element abs 1e-6 + rel 1e-6 against the double GELU_tanh"}
         ops[-1].verify = verify_bias
+        ops[-1].cpu_ref = lambda ref, hxb=hxb, hbb=hbb, br=br, bc=bc: ref.bias_act(hxb, hbb, br,
+                                                                                 bc, 3)
 
     # --- calibration: a plain copy of known size (only when asked for) -------
     if only is not None and want("copy_256mib"):
@@ -592,43 +599,65 @@ def gemm_lp_section(m, stream, iters=10, with_peak=True):
     return out, verifies
 
 
-def graph_section(m, steps=5, warmup=2):
+def graph_section(m, steps=5, warmup=2, gate_repeats=20):
     """BASELINE config 5 through the GraphExecutor (buddy allocator, chain-greedy
     schedule, happens-before arena reuse):
       * the MLP block X[4096x4096] -> GEMM(W1 4096x16384) -> bias+GELU -> GEMM(W2)
         -> bias -> softmax, per-node times and roofline fractions;
-      * a 4x4 fan-out of 2048^3 GEMM chains on 4 streams vs the same graph on one
-        stream, with the overlap (sum of node times / wall) and buddy statistics."""
+      * a 4x4 fan-out of 2048^3 GEMM chains on 4 streams (chain-greedy and
+        level-parallel) vs the same graph on one stream, with the overlap (sum of
+        node times / wall) and buddy statistics;
+      * the reference graph bench's diamond of 2048^3 GEMMs and its chain of 16
+        bias+GELU nodes on 4096x4096, under the three schedules;
+      * for every timed plan the launch-bound ratio (host enqueue time of one
+        run / device time of one run, bench/graph_bench.cpp:437-441).
+    At both config-5 shapes it also runs the numerics gate (3 schedules x 3 memory
+    policies x `gate_repeats`, bench/graph_bench.cpp:444-471) and reads every
+    stage of a per-tensor plan back to the host.  Returns (results, verify), where
+    verify(oracle) checks those stages in the CPU leg and stores the outcome under
+    results[*]["parity"]."""
     from mcke_amd import graph as G
 
     out = {}
+    host = {}
 
     def timed_runs(ex, n):
+        """Average device ms per run over n back-to-back runs, and the median host
+        time (us) one run_async call takes to enqueue its launches."""
         st = ex.stream()
         e0, e1 = m.Event(), m.Event()
         for _ in range(warmup):
             ex.run_async()
         ex.synchronize()
+        enq = []
         e0.record(st)
         for _ in range(n):
+            t0 = time.perf_counter()
             ex.run_async()
+            enq.append(time.perf_counter() - t0)
         e1.record(st)
         ex.synchronize()
-        return e0.elapsed_ms(e1) / n
+        return e0.elapsed_ms(e1) / n, float(np.median(enq)) * 1e6
+
+    def launch_bound(wall_ms, enqueue_us):
+        return round((enqueue_us / 1e3) / wall_ms, 4)
 
     T, D, F = 4096, 4096, 16384
     log("config 5: MLP block 4096x4096 -> 16384 -> 4096")
+    mlp_in = {"x": m.fill_normal(T * D, 0x3001, 0.0, 1.0),
+              "W1": m.fill_normal(D * F, 0x3002, 0.0, 0.02),
+              "b1": m.fill_normal(F, 0x3003, 0.0, 0.01),
+              "W2": m.fill_normal(F * D, 0x3004, 0.0, 0.02),
+              "b2": m.fill_normal(D, 0x3005, 0.0, 0.01)}
     g, t = G.mlp_block(T, D, F)
     ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, schedule=G.SchedulePolicy.kChainGreedy,
                     memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4, profile=True,
                     profile_slots=warmup + steps)
     ex.plan()
-    ex.set_input(t["x"], m.fill_normal(T * D, 0x3001, 0.0, 1.0))
-    ex.set_input(t["W1"], m.fill_normal(D * F, 0x3002, 0.0, 0.02))
-    ex.set_input(t["b1"], m.fill_normal(F, 0x3003, 0.0, 0.01))
-    ex.set_input(t["W2"], m.fill_normal(F * D, 0x3004, 0.0, 0.02))
-    ex.set_input(t["b2"], m.fill_normal(D, 0x3005, 0.0, 0.01))
-    wall = timed_runs(ex, steps)
+    for k, v in mlp_in.items():
+        ex.set_input(t[k], v)
+    wall, enq = timed_runs(ex, steps)
+    y_timed = ex.read(t["y"], T * D)
     info = ex.plan_info()
     nodes = []
     for x in ex.timings():
@@ -644,6 +673,7 @@ def graph_section(m, steps=5, warmup=2):
     ex.plan()     # re-plan: the new arena comes from the block the old one returned
     out["mlp_block"] = {
         "shape": f"X[{T}x{D}] W1[{D}x{F}] W2[{F}x{D}]", "wall_ms": round(wall, 4),
+        "enqueue_us": round(enq, 2), "launch_bound_ratio": launch_bound(wall, enq),
         "tflops": round(info["total_flops"] / (wall * 1e-3) / 1e12, 2),
         "roofline_bound_ms": round(bound_ms, 4), "bound_over_wall": round(bound_ms / wall, 4),
         "nodes": nodes, "arena_bytes": info["arena_bytes"], "naive_bytes": info["naive_bytes"],
@@ -652,19 +682,55 @@ def graph_section(m, steps=5, warmup=2):
     log(f"config 5 MLP: {wall:.3f} ms/run, {out['mlp_block']['tflops']} TFLOP/s")
     ex.close()
 
+    # Parity material: every stage of a per-tensor plan (checked in the CPU leg),
+    # the timed plan's output bits against it, and the numerics gate.
+    g, t = G.mlp_block(T, D, F)
+    ex = G.Executor(g, schedule=G.SchedulePolicy.kSequential,
+                    memory=G.MemoryPolicy.kAllocPerTensor, num_streams=1)
+    ex.plan()
+    for k, v in mlp_in.items():
+        ex.set_input(t[k], v)
+    ex.run_sync()
+    host["mlp"] = {"gemm1": ex.read(t["gemm1"], T * F), "h": ex.read(t["h"], T * F),
+                   "gemm2": ex.read(t["gemm2"], T * D), "z": ex.read(t["z"], T * D),
+                   "y": ex.read(t["y"], T * D)}
+    ex.close()
+    same_bits = bool(np.array_equal(y_timed.view(np.uint32), host["mlp"]["y"].view(np.uint32)))
+    del y_timed
+    g, t = G.mlp_block(T, D, F)
+    ex = G.Executor(g, num_streams=4, validate_numerics=True)
+    ex.plan()
+    for k, v in mlp_in.items():
+        ex.set_input(t[k], v)
+    gate = ex.validate_numerics(repeats=gate_repeats)
+    ex.close()
+    out["mlp_block"]["gate"] = {"passed": gate.passed, "configs": gate.configs_compared,
+                                "repeats": gate_repeats, "detail": gate.detail}
+    out["mlp_block"]["timed_plan_same_bits_as_per_tensor_plan"] = same_bits
+    log(f"config 5 MLP: numerics gate {'PASS' if gate.passed else 'FAIL'}, timed plan same "
+        f"bits: {same_bits}")
+
     n, B, Dp = 2048, 4, 4
+    fan_n = n
+    fan_w = m.fill_random(n * n, 0x4000, -0.03125, 0.03125)
+    fan_xs = [m.fill_random(n * n, 0x4001 + k) for k in range(B)]
+
+    def fanout_executor(sched, streams, memory=G.MemoryPolicy.kReuseHappensBefore, **kw):
+        g, t = G.gemm_fanout(B, Dp, n)
+        ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, schedule=sched, memory=memory,
+                        num_streams=streams, **kw)
+        ex.plan()
+        ex.set_input(t["W"], fan_w)
+        for k in range(B):
+            ex.set_input(t["xs"][k], fan_xs[k])
+        return ex, t
+
     fan = {}
     for label, sched, streams in (("sequential", G.SchedulePolicy.kSequential, 1),
+                                  ("level_parallel_4streams", G.SchedulePolicy.kLevelParallel, 4),
                                   ("chain_greedy_4streams", G.SchedulePolicy.kChainGreedy, 4)):
-        g, t = G.gemm_fanout(B, Dp, n)
-        ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, schedule=sched,
-                        memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=streams,
-                        profile=True, profile_slots=warmup + steps)
-        ex.plan()
-        ex.set_input(t["W"], m.fill_random(n * n, 0x4000, -0.03125, 0.03125))
-        for k in range(B):
-            ex.set_input(t["xs"][k], m.fill_random(n * n, 0x4001 + k))
-        wall = timed_runs(ex, steps)
+        ex, _ = fanout_executor(sched, streams, profile=True, profile_slots=warmup + steps)
+        wall, enq = timed_runs(ex, steps)
         tim = ex.timings()
         node_sum = sum(x["median_ms"] for x in tim)
         info = ex.plan_info()
@@ -672,14 +738,78 @@ def graph_section(m, steps=5, warmup=2):
         fan[label] = {"wall_ms": round(wall, 4), "node_sum_ms": round(node_sum, 4),
                       "overlap": round(node_sum / wall, 3),
                       "tflops": round(info["total_flops"] / (wall * 1e-3) / 1e12, 2),
+                      "enqueue_us": round(enq, 2), "launch_bound_ratio": launch_bound(wall, enq),
                       "streams": info["num_streams_used"], "events": info["num_events"],
                       "waits": info["waits_dedup"], "arena_bytes": info["arena_bytes"],
                       "allocator": ex.allocator_stats()}
         log(f"config 5 fan-out {label}: {wall:.3f} ms, overlap {node_sum / wall:.2f}")
         ex.close()
-    fan["speedup_vs_sequential"] = round(fan["sequential"]["wall_ms"] /
-                                         fan["chain_greedy_4streams"]["wall_ms"], 3)
+    for label in ("level_parallel_4streams", "chain_greedy_4streams"):
+        fan[label]["speedup_vs_sequential"] = round(fan["sequential"]["wall_ms"] /
+                                                    fan[label]["wall_ms"], 3)
+    fan["speedup_vs_sequential"] = fan["chain_greedy_4streams"]["speedup_vs_sequential"]
+    ex, t = fanout_executor(G.SchedulePolicy.kChainGreedy, 4, memory=G.MemoryPolicy.kAllocPerTensor)
+    ex.run_sync()
+    host["fan"] = [[ex.read(tid, n * n) for tid in chain] for chain in t["nodes"]]
+    ex.close()
+    ex, _ = fanout_executor(G.SchedulePolicy.kChainGreedy, 4, validate_numerics=True)
+    gate = ex.validate_numerics(repeats=gate_repeats)
+    ex.close()
+    fan["gate"] = {"passed": gate.passed, "configs": gate.configs_compared,
+                   "repeats": gate_repeats, "detail": gate.detail}
+    log(f"config 5 fan-out: numerics gate {'PASS' if gate.passed else 'FAIL'}")
     out["fanout4x4_gemm2048"] = fan
+
+    # The reference graph bench's other topologies (bench/graph_bench.cpp:100-166):
+    # a diamond of 2048^3 GEMMs (B and C from A, D from both) and a chain of 16
+    # bias+GELU nodes over X[4096 x 4096], each under the three schedules.
+    def diamond_gemm(nn):
+        g = G.Graph()
+        a = g.add_input((nn, nn), "A")
+        w = g.add_input((nn, nn), "W")
+        left = g.add_gemm(a, w, "B_gemm")
+        right = g.add_gemm(a, w, "C_gemm")
+        g.mark_output(g.add_gemm(left, right, "D_gemm"))
+        return g, {"A": (a, m.fill_random(nn * nn, 0x4200, -0.0625, 0.0625)),
+                   "W": (w, m.fill_random(nn * nn, 0x4201, -0.0625, 0.0625))}
+
+    def chain16(rows, cols):
+        g = G.Graph()
+        x = g.add_input((rows, cols), "x")
+        bias = g.add_input((cols,), "bias")
+        cur = x
+        for i in range(16):
+            cur = g.add_bias_act(cur, bias, f"n{i}", act=3)
+        g.mark_output(cur)
+        return g, {"x": (x, m.fill_normal(rows * cols, 0x4300)),
+                   "bias": (bias, m.fill_random(cols, 0x4301, -0.5, 0.5))}
+
+    ref_graphs = {}
+    for gname, build in (("diamond_gemm_2048", lambda: diamond_gemm(2048)),
+                         ("chain16_4096x4096", lambda: chain16(4096, 4096))):
+        rows = {}
+        for label, sched, streams in (("sequential", G.SchedulePolicy.kSequential, 1),
+                                      ("level_parallel", G.SchedulePolicy.kLevelParallel, 4),
+                                      ("chain_greedy", G.SchedulePolicy.kChainGreedy, 4)):
+            g, inputs = build()
+            ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, schedule=sched,
+                            memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=streams)
+            ex.plan()
+            for tid, arr in inputs.values():
+                ex.set_input(tid, arr)
+            wall, enq = timed_runs(ex, steps)
+            info = ex.plan_info()
+            rows[label] = {"wall_ms": round(wall, 4), "enqueue_us": round(enq, 2),
+                           "launch_bound_ratio": launch_bound(wall, enq),
+                           "streams": info["num_streams_used"], "events": info["num_events"],
+                           "arena_bytes": info["arena_bytes"], "naive_bytes": info["naive_bytes"]}
+            ex.close()
+        for label in ("level_parallel", "chain_greedy"):
+            rows[label]["speedup_vs_sequential"] = round(rows["sequential"]["wall_ms"] /
+                                                         rows[label]["wall_ms"], 3)
+        ref_graphs[gname] = rows
+        log(f"graph {gname}: " + ", ".join(f"{k} {v['wall_ms']:.3f} ms" for k, v in rows.items()))
+    out["reference_graphs"] = ref_graphs
 
     # Launch-bound shapes: the same MLP chain at small sizes, replayed eagerly (the
     # plan's launches issued by the host each run) and as one captured HIP graph
@@ -700,7 +830,7 @@ def graph_section(m, steps=5, warmup=2):
             ex.set_input(t["b2"], m.fill_normal(D2, 0x3105, 0.0, 0.01))
             if label == "hip_graph":
                 ex.capture()
-            wall = timed_runs(ex, 200)
+            wall, _ = timed_runs(ex, 200)
             y = ex.read(t["y"], T2 * D2)
             cap[label] = {"us_per_run": round(wall * 1e3, 2), "y_bits": y.view(np.uint32)}
             ex.close()
@@ -731,7 +861,7 @@ def graph_section(m, steps=5, warmup=2):
                 ex.set_input(t["xs"][k], m.fill_random(n * n, 0x4101 + k))
             if label == "hip_graph":
                 ex.capture()
-            wall = timed_runs(ex, 200)
+            wall, _ = timed_runs(ex, 200)
             bits_seen.append(np.concatenate([ex.read(o, n * n).view(np.uint32) for o in t["outs"]]))
             cap[label] = {"us_per_run": round(wall * 1e3, 2)}
             ex.close()
@@ -741,19 +871,37 @@ def graph_section(m, steps=5, warmup=2):
             f"hipGraph {cap['hip_graph']['us_per_run']} us per run")
     fan_cap["same_bits"] = all(np.array_equal(bits_seen[0], b) for b in bits_seen[1:])
     out["fanout_small_capture"] = fan_cap
-    return out
+
+    def verify(orc):
+        from oracle import graph_checks as gc
+        mlp = gc.check_mlp(mlp_in, host["mlp"], T, D, F)
+        mlp["ok"] = bool(mlp["ok"] and same_bits and out["mlp_block"]["gate"]["passed"])
+        out["mlp_block"]["parity"] = mlp
+        fp = gc.check_fanout(fan_w, fan_xs, host["fan"], fan_n)
+        fp["ok"] = bool(fp["ok"] and out["fanout4x4_gemm2048"]["gate"]["passed"])
+        out["fanout4x4_gemm2048"]["parity"] = fp
+        return {"ok": mlp["ok"] and fp["ok"]}
+
+    return out, verify
 
 
-def cpu_baseline(m, gemm_bufs, seconds_target=12.0, stream=None):
-    """The CPU reference GEMM (reference tests/reference.hpp:199-211: i-j-p loops,
-    double accumulation, one thread) on a row slab of the same 8192^3 problem,
-    and a parity check of the GPU's C on that slab.  Uses oracle/_ref (the
-    reference's own code) when it was built, else the plain-C restatement.
+def cpu_baseline(m, gemm_bufs, ops, seconds_target=10.0, stream=None, runs=5):
+    """The CPU reference, one thread, timed on this host beside the GPU run.  Uses
+    oracle/_ref (the reference's own tests/reference.hpp, compiled from its
+    sources) when it was built, else the plain-C restatement.
 
-    Beside it: the full reference at 512^3 and 1024^3 (configs[0]'s smallest
-    sweep sizes) against the GPU's C at those sizes, and the same row-slab work
-    split by rows over the host cores (one reference call per thread; ctypes
-    releases the GIL), reported as a separate figure."""
+    GEMM (reference.hpp:199-211: i-j-p loops, double accumulation): a row slab of
+    the same 8192^3 problem, sized so that `runs` runs take about
+    `seconds_target`, timed `runs` times (median and min), and the GPU's C
+    checked on that slab.  Beside it: the full reference at 512^3 and 1024^3
+    against the GPU's C at those sizes, and the slab's work split by rows over
+    the host cores (one reference call per thread; ctypes releases the GIL),
+    reported as a separate figure.
+
+    Every memory-bound op of the step (row sum/max, full sum, softmax, bias+GELU)
+    at its full BASELINE shape on the op's own input: reference_row_reduce,
+    reference_row_softmax and reference_bias_act (reference.hpp:143-191), each
+    timed `runs` times, median and min, with GB/s at the op's algorithmic bytes."""
     import concurrent.futures
     import oracle
 
@@ -763,29 +911,49 @@ def cpu_baseline(m, gemm_bufs, seconds_target=12.0, stream=None):
     hc = c.download(n * n)
     use_ref = oracle.ref_available()
     kind = "reference" if use_ref else "port"
-    # Time one row first, then size the slab to ~seconds_target.
-    rows_done, elapsed = 0, 0.0
-    slab_rows = 1
-    want_rows = []
-    while elapsed < seconds_target and rows_done < n:
-        r0, r1 = rows_done, min(n, rows_done + slab_rows)
-        sa = ha[r0 * n:r1 * n]
-        out = np.zeros((r1 - r0) * n, np.float32)
+    ref = oracle.Ref if use_ref else oracle
+    host_cores = os.cpu_count()
+    ref_gemm = ref.gemm
+
+    # Size the slab from one row, then time the same slab `runs` times.
+    t = time.perf_counter()
+    ref_gemm(ha[:n], hb, np.zeros(n, np.float32), 1, n, n, 1.0, 0.0)
+    per_row = time.perf_counter() - t
+    rows_done = max(1, min(64, int(seconds_target / runs / per_row)))
+    times, want = [], None
+    for _ in range(runs):
+        out = np.zeros(rows_done * n, np.float32)
         t = time.perf_counter()
-        if use_ref:
-            got = oracle.Ref.gemm(sa, hb, out, r1 - r0, n, n, 1.0, 0.0)
-        else:
-            got = oracle.gemm(sa, hb, out, r1 - r0, n, n, 1.0, 0.0)
-        elapsed += time.perf_counter() - t
-        want_rows.append(got)
-        rows_done = r1
-        per_row = elapsed / rows_done
-        slab_rows = max(1, min(64, int((seconds_target - elapsed) / per_row)))
-    want = np.concatenate(want_rows)
-    got = hc[:rows_done * n]
-    r = oracle.compare(got, want, oracle.tol_gemm(n), oracle.abs_tol_gemm(n))
+        got_rows = ref_gemm(ha[:rows_done * n], hb, out, rows_done, n, n, 1.0, 0.0)
+        times.append(time.perf_counter() - t)
+        if want is None:
+            want = got_rows
+    tarr = np.array(times)
+    elapsed = float(np.median(tarr))
+    r = oracle.compare(hc[:rows_done * n], want, oracle.tol_gemm(n), oracle.abs_tol_gemm(n))
     flops = 2.0 * rows_done * n * n
-    ref_gemm = oracle.Ref.gemm if use_ref else oracle.gemm
+    log(f"cpu baseline: GEMM slab {rows_done}x{n}x{n}: median {elapsed:.2f} s, min "
+        f"{tarr.min():.2f} s over {runs} runs")
+
+    # The memory-bound ops at their full shapes.
+    op_rows = []
+    for op in ops:
+        if op.cpu_ref is None:
+            continue
+        ts = []
+        for _ in range(runs):
+            t = time.perf_counter()
+            op.cpu_ref(ref)
+            ts.append(time.perf_counter() - t)
+        ts = np.array(ts)
+        med = float(np.median(ts))
+        op_rows.append({"name": op.name, "shape": op.shape, "runs": runs,
+                        "median_ms": round(med * 1e3, 2), "min_ms": round(float(ts.min()) * 1e3, 2),
+                        "gb_s": round(op.work / med / 1e9, 3),
+                        "gpu_speedup": round(med * 1e3 / (op.total_ms / op.launches), 1)
+                        if op.launches else None})
+        log(f"cpu baseline: {op.name} median {med * 1e3:.1f} ms "
+            f"({op.work / med / 1e9:.2f} GB/s), min {ts.min() * 1e3:.1f} ms")
 
     # The full reference at 512^3 and 1024^3, on bench inputs of those sizes.
     full = []
@@ -825,9 +993,11 @@ def cpu_baseline(m, gemm_bufs, seconds_target=12.0, stream=None):
     return {
         "value": round(flops / elapsed / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
         "kind": kind,
-        "sample": f"rows 0..{rows_done - 1} of C for the 8192^3 GEMM ({rows_done}x8192x8192, "
-                  f"{elapsed:.1f} s, 1 thread of {os.cpu_count()} host cores, double "
-                  f"accumulation in the reference's i-j-p order)",
+        "sample": f"rows 0..{rows_done - 1} of C for the 8192^3 GEMM ({rows_done}x8192x8192), "
+                  f"median of {runs} runs, 1 thread of {host_cores} host cores, double "
+                  f"accumulation in the reference's i-j-p order",
+        "gemm_slab_seconds": {"median": round(elapsed, 3), "min": round(float(tarr.min()), 3),
+                              "runs": runs},
         "extrapolated_8192_s": round(elapsed / rows_done * n, 1),
         "parity_on_sample": {"ok": bool(r.ok), "max_abs_err": r.max_abs_err,
                              "max_rel_err": r.max_rel_err,
@@ -838,6 +1008,10 @@ def cpu_baseline(m, gemm_bufs, seconds_target=12.0, stream=None):
                          "seconds": round(dt_par, 2),
                          "tflops": round(2.0 * threads * n * n / dt_par / 1e12, 6),
                          "parity_ok": bool(rp.ok)},
+        "ops": op_rows,
+        "ops_note": f"memory-bound ops at their full BASELINE shapes on the ops' own inputs, "
+                    f"1 thread of {host_cores} host cores, {runs} runs each; gpu_speedup = CPU "
+                    f"median / GPU average launch",
     }
 
 
@@ -848,7 +1022,8 @@ def main(argv=None) -> int:
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-sweep", action="store_true", help="skip the GEMM size sweep")
-    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="target CPU time of the GEMM slab's timed runs together")
     p.add_argument("--no-graph", action="store_true", help="skip the config-5 graph section")
     p.add_argument("--no-peaks", action="store_true", help="skip the measured-peak microbenches")
     p.add_argument("--no-lp", action="store_true", help="skip the 16-bit-input GEMM section")
@@ -905,7 +1080,9 @@ def main(argv=None) -> int:
     lp_res, lp_verify = None, []
     if not args.no_lp and (only is None or any(x.startswith("gemm_lp") for x in only)):
         lp_res, lp_verify = gemm_lp_section(m, stream, with_peak=not args.no_peaks)
-    graph_res = None if (args.no_graph or only is not None) else graph_section(m)
+    graph_res, graph_verify = None, None
+    if not (args.no_graph or only is not None):
+        graph_res, graph_verify = graph_section(m)
     cpu = None
     if not args.no_cpu:
         # The CPU checker on every timed op's output at its timed shape (the timed
@@ -917,14 +1094,18 @@ def main(argv=None) -> int:
                 op.parity = op.verify(oracle)
                 log(f"parity {op.name}: {'OK' if op.parity['ok'] else 'FAILED'} "
                     f"({time.perf_counter() - t0:.1f} s)")
-        for name, verify in lp_verify:
+        extra = list(lp_verify)
+        if graph_verify is not None:
+            extra.append(("graph (config 5 stages, timed-plan bits, numerics gates)", graph_verify))
+        for name, verify in extra:
             t0 = time.perf_counter()
             res = verify(oracle)
             log(f"parity {name}: {'OK' if res['ok'] else 'FAILED'} "
                 f"({time.perf_counter() - t0:.1f} s)")
     if not args.no_cpu and gemm_bufs[0] is not None:
-        log(f"cpu baseline: reference GEMM on a row slab (~{args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline(m, gemm_bufs, args.cpu_seconds, stream)
+        log(f"cpu baseline: reference GEMM on a row slab (~{args.cpu_seconds:.0f} s) and the "
+            "memory-bound ops at full shape")
+        cpu = cpu_baseline(m, gemm_bufs, ops, args.cpu_seconds, stream)
         log(f"cpu baseline: {cpu['value']} TFLOP/s ({cpu['sample']})")
     summaries = [op.summary(s["measured_peak"] if "measured_peak" in s else None,
                             s.get("hbm_traffic_bytes")) for op, s in zip(ops, summaries)]

@@ -338,15 +338,19 @@ def mlp_block(tokens: int, d_model: int, d_ff: int, gemm_variant=GemmVariant.kMf
 def gemm_fanout(branches: int, depth: int, n: int, gemm_variant=GemmVariant.kMfmaF32):
     """`branches` independent chains of `depth` n^3 GEMMs: chain k is
     C_k0 = X_k W, C_kd = C_k(d-1) W (the reference's fanout topology,
-    graph_bench.cpp:176-194, with GEMM nodes)."""
+    graph_bench.cpp:176-194, with GEMM nodes).  The returned "nodes"[k][d] is the
+    output of GEMM d of chain k."""
     g = Graph()
     w = g.add_input((n, n), "W")
-    xs, outs = [], []
+    xs, outs, nodes = [], [], []
     for k in range(branches):
         cur = g.add_input((n, n), f"x{k}")
         xs.append(cur)
+        chain = []
         for d in range(depth):
             cur = g.add_gemm(cur, w, f"b{k}g{d}", gemm_variant)
+            chain.append(cur)
         g.mark_output(cur)
         outs.append(cur)
-    return g, {"W": w, "xs": xs, "outs": outs}
+        nodes.append(chain)
+    return g, {"W": w, "xs": xs, "outs": outs, "nodes": nodes}

@@ -190,6 +190,47 @@ def _eager_y(G, inp, T, D, F, **kw):
     return y
 
 
+def test_memset_refused_under_capture(gpu):
+    """mcke_rt_memset_async refuses a stream that is being captured (a memset node
+    does not replay reliably on this stack) and names the fill kernel; the fill
+    kernel captured in its place replays right, three times, with an eager memset
+    of the same buffer between replays."""
+    import ctypes as C
+
+    m = gpu
+    L = m.lib()
+    VP = C.c_void_p
+    for name, args in (("mcke_rt_stream_begin_capture", [VP]),
+                       ("mcke_rt_stream_end_capture", [VP, C.POINTER(VP)]),
+                       ("mcke_rt_graph_launch", [VP, VP]),
+                       ("mcke_rt_graph_destroy", [VP]),
+                       ("mcke_fill_u32_async", [VP, C.c_uint32, C.c_size_t, VP])):
+        getattr(L, name).restype = C.c_int
+        getattr(L, name).argtypes = args
+    n = 4096
+    buf = m.DeviceBuffer(n * 4)
+    st = m.Stream()
+    exe = VP()
+    try:
+        assert L.mcke_rt_stream_begin_capture(st.handle) == 0
+        rc = L.mcke_rt_memset_async(buf.ptr, 0, n * 4, st.handle)
+        msg = L.mcke_last_error().decode()
+        assert L.mcke_fill_u32_async(buf.ptr, 0x3F800000, n, st.handle) == 0
+        assert L.mcke_rt_stream_end_capture(st.handle, C.byref(exe)) == 0 and exe.value
+        assert rc == int(m.StatusCode.kInvalidArgument), rc
+        assert "mcke_fill_u32_async" in msg, msg
+        for _ in range(3):
+            buf.memset(0, st)                 # eager, not captured: allowed
+            st.synchronize()
+            assert L.mcke_rt_graph_launch(exe, st.handle) == 0
+            got = buf.download(n, stream=st)
+            assert np.all(got == 1.0)
+    finally:
+        if exe.value:
+            L.mcke_rt_graph_destroy(exe)
+        st.close()
+
+
 @pytest.mark.parametrize("poison", [False, True])
 def test_captured_replays_match_eager(G, orc, poison):
     """Every replay of the captured iteration gives the eager bits, with the

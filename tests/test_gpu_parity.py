@@ -231,6 +231,26 @@ def test_gemm_beta_zero_never_reads_c(gpu, orc):
         assert r.ok, f"{cfg_id(cfg)}: {r}"
 
 
+@pytest.mark.parametrize("shape", [(256, 256), (70, 90)])
+def test_gemm_k_zero(gpu, orc, shape):
+    """k == 0 launches the kernel and gives C = beta * C (reference gemm.cu:867, no
+    early return), for every variant and tile: beta = 2 doubles C exactly (also
+    against the oracle), and beta = 0 on a NaN-poisoned C gives zeros (C is not
+    read).  256 x 256 is whole tiles for every MFMA tile, 70 x 90 is ragged."""
+    M, N = shape
+    c = orc.fill_random(M * N, 0xC0FFEE)
+    empty = np.zeros(0, np.float32)
+    want = orc.gemm(empty, empty, c, M, N, 0, 1.0, 2.0)
+    assert np.array_equal(golden_io.bits(want), golden_io.bits(c * np.float32(2.0)))
+    poisoned = np.full(M * N, np.nan, np.float32)
+    zeros = np.zeros(M * N, np.float32)
+    for cfg in gemm_configs(gpu):
+        got = run_gemm(gpu, empty, empty, c, M, N, 0, 1.0, 2.0, *cfg)
+        assert np.array_equal(golden_io.bits(got), golden_io.bits(want)), cfg_id(cfg)
+        got = run_gemm(gpu, empty, empty, poisoned, M, N, 0, 1.0, 0.0, *cfg)
+        assert np.array_equal(golden_io.bits(got), golden_io.bits(zeros)), cfg_id(cfg)
+
+
 @pytest.mark.parametrize("size", [512, 1024])
 def test_gemm_quarter_exact_mfma(gpu, size):
     """Quarter-multiple inputs: the exact product is representable in f32 and any
