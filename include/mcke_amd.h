@@ -152,6 +152,16 @@ int mcke_launch_row_reduce_ws_f32(const float* x, float* out, int64_t rows, int6
                                   int kind, int variant, float* workspace,
                                   size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference: kTwoPass (the 9-argument launch above, same
+ * kernels, same bits) for callers that cannot allocate -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  It takes no
+ * workspace and allocates nothing: the split partials go to a 4 KiB device array
+ * the library holds per GPU (1024 partials; this build's split needs at most
+ * 511, and a shape needing more is INVALID_ARGUMENT).  Calls that overlap on one
+ * GPU share that array and race; calls in one stream's order do not. */
+int mcke_launch_row_reduce_noalloc_f32(const float* x, float* out, int64_t rows, int64_t cols,
+                                       int kind, void* stream);
+
 /* launch_row_softmax_f32, kernels.hpp:220-223 / softmax.cu:177-199.  x == y
  * rejected; rows > 2^31-1 rejected. */
 int mcke_launch_row_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols,

@@ -179,6 +179,7 @@ def lib() -> C.CDLL:
         "mcke_launch_row_reduce_f32": (C.c_int, [_VP, _VP, _I64, _I64, C.c_int, C.c_int, _VP]),
         "mcke_launch_row_reduce_ws_f32": (C.c_int, [_VP, _VP, _I64, _I64, C.c_int, C.c_int,
                                                     _VP, C.c_size_t, _VP]),
+        "mcke_launch_row_reduce_noalloc_f32": (C.c_int, [_VP, _VP, _I64, _I64, C.c_int, _VP]),
         "mcke_launch_row_softmax_f32": (C.c_int, [_VP, _VP, _I64, _I64, C.c_int, _VP]),
         "mcke_launch_gemm_f32": (C.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, C.c_float,
                                            C.c_float, C.c_int, C.POINTER(GemmTile), _VP]),
@@ -484,6 +485,13 @@ def launch_row_reduce_f32(x, out, rows: int, cols: int, kind, variant, *rest) ->
     return _st(lib().mcke_launch_row_reduce_ws_f32(_ptr(x), _ptr(out), rows, cols, int(kind),
                                                    int(variant), _ptr(workspace), ws_bytes,
                                                    _sh(stream)))
+
+
+def launch_row_reduce_noalloc_f32(x, out, rows: int, cols: int, kind, stream=None) -> Status:
+    """kTwoPass without a workspace and without allocating (no reference
+    counterpart): the partials live in a per-GPU device array of the library."""
+    return _st(lib().mcke_launch_row_reduce_noalloc_f32(_ptr(x), _ptr(out), rows, cols, int(kind),
+                                                        _sh(stream)))
 
 
 def launch_row_softmax_f32(x, y, rows: int, cols: int, variant, stream=None) -> Status:

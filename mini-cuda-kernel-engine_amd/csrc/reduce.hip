@@ -26,6 +26,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -261,6 +262,38 @@ int dispatch_two_pass(const float* x, float* out, int64_t rows, int64_t cols, in
   }
 }
 
+// The partials of mcke_launch_row_reduce_noalloc_f32, for callers that cannot
+// allocate: one array per GPU the library runs on, held until the process ends.
+// 1024 floats (4 KiB); under two_pass_split a call needs at most
+// rows * split <= 511 of them (rows <= 256 split into ceil(256 / rows) chunks,
+// more rows are not split).  Every call on a GPU shares its array; the
+// partials are written before they are read, so nothing in it has to start at
+// zero, but calls that overlap on one GPU race.
+constexpr int64_t kScratchFloats = 1024;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's copy of `scratch`, as a device address.  Looked up once per
+// device, with that device current: in host code the array's name is a host
+// stand-in, not a device address.
+int scratch_of_current_device(float** out) {
+  int dev = -1;
+  MCKE_HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices)
+    return invalid("launch_row_reduce_noalloc_f32: device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    MCKE_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return ok();
+}
+
 }  // namespace
 }  // namespace mcke_amd
 
@@ -303,6 +336,25 @@ int mcke_launch_row_reduce_ws_f32(const float* x, float* out, int64_t rows, int6
     case MCKE_REDUCE_MEAN: return launch_one_pass<SumOp, true>(x, out, rows, cols, tree, st);
     default: return launch_one_pass<MaxOp, false>(x, out, rows, cols, tree, st);
   }
+}
+
+int mcke_launch_row_reduce_noalloc_f32(const float* x, float* out, int64_t rows, int64_t cols,
+                                       int kind, void* stream) {
+  if (rows == 0 || cols == 0) return ok();
+  if (rows < 0 || cols < 0) return invalid("launch_row_reduce_noalloc_f32: negative extent");
+  if (!x || !out) return invalid("launch_row_reduce_noalloc_f32: null pointer");
+  if (kind < 0 || kind > 2) return invalid("launch_row_reduce_noalloc_f32: unknown ReduceKind");
+  if (rows > 65535)
+    return invalid("launch_row_reduce_noalloc_f32: rows exceed the grid's y limit (65535)");
+  const int64_t split = two_pass_split(rows, cols);
+  const int64_t partials = split > 1 ? rows * split : 0;
+  if (partials > kScratchFloats)
+    return invalid("launch_row_reduce_noalloc_f32: needs " + std::to_string(partials) +
+                   " partials, more than the " + std::to_string(kScratchFloats) +
+                   " its scratch holds; use launch_row_reduce_f32 with a workspace");
+  float* part = nullptr;
+  if (const int rc = scratch_of_current_device(&part)) return rc;
+  return dispatch_two_pass(x, out, rows, cols, kind, part, static_cast<hipStream_t>(stream));
 }
 
 int mcke_launch_row_reduce_f32(const float* x, float* out, int64_t rows, int64_t cols, int kind,
