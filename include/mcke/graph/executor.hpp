@@ -5,16 +5,17 @@
 // executor.cpp:39-619:
 //   plan()       finalize, schedule (plan_streams + verify_plan_ordering),
 //                happens-before, memory plan (+ verify_no_buffer_races), create
-//                streams / events / arena / per-stream workspaces, bind tensors;
-//   run_async()  fork (stream 0 records, the others wait), per node: its waits,
-//                optional timing probes, Op::launch, its record; join back onto
-//                stream 0.  Never synchronises the host.  With poison_buffers the
-//                arena (outside the input ranges) is refilled each run with a
-//                pattern that changes per iteration;
+//                streams / events / arena / per-stream workspaces, bind tensors,
+//                and compile one iteration into a list of host steps;
+//   run_async()  issues that list: fork (stream 0 records, the others wait), per
+//                node its waits, optional timing stamps, Op::launch and its
+//                record, then the join back onto stream 0.  Never synchronises
+//                the host.  With poison_buffers the arena (outside the graph
+//                inputs) is refilled first with a pattern that changes per run;
 //   validate_numerics()  runs {sequential, level-parallel, chain-greedy} x
 //                {per-tensor, same-stream, happens-before} plans `repeats` times
 //                each with poisoning on and requires every output to be bitwise
-//                identical to the sequential/per-tensor golden run.
+//                identical to the sequential/per-tensor run.
 #pragma once
 
 #include <cstdint>
@@ -81,43 +82,53 @@ struct ScheduledNode {
 class ExecutionPlan {
  public:
   [[nodiscard]] const std::vector<ScheduledNode>& nodes() const noexcept { return sched_; }
-  [[nodiscard]] std::size_t num_streams() const noexcept { return streams_.size(); }
-  [[nodiscard]] std::size_t peak_memory_bytes() const noexcept { return peak_bytes_; }
-  [[nodiscard]] std::size_t naive_memory_bytes() const noexcept { return naive_bytes_; }
+  [[nodiscard]] std::size_t num_streams() const noexcept { return lanes_.size(); }
+  [[nodiscard]] std::size_t peak_memory_bytes() const noexcept { return arena_bytes_; }
+  [[nodiscard]] std::size_t naive_memory_bytes() const noexcept { return unshared_bytes_; }
   [[nodiscard]] const std::vector<std::uint32_t>& wait_pool() const noexcept { return wait_pool_; }
   [[nodiscard]] std::string describe() const;
-  [[nodiscard]] const StreamAssignment& stream_plan() const noexcept { return streams_plan_; }
-  [[nodiscard]] const MemoryPlan& memory_plan() const noexcept { return memory_plan_; }
-  [[nodiscard]] std::size_t intra_events() const noexcept { return streams_plan_.num_events; }
-  [[nodiscard]] std::size_t intra_waits() const noexcept { return streams_plan_.waits_dedup; }
+  [[nodiscard]] const StreamAssignment& stream_plan() const noexcept { return schedule_; }
+  [[nodiscard]] const MemoryPlan& memory_plan() const noexcept { return memory_; }
+  [[nodiscard]] std::size_t intra_events() const noexcept { return schedule_.num_events; }
+  [[nodiscard]] std::size_t intra_waits() const noexcept { return schedule_.waits_dedup; }
   [[nodiscard]] std::size_t forkjoin_events() const noexcept {
-    const std::size_t k = streams_plan_.num_streams_used;
+    const std::size_t k = schedule_.num_streams_used;
     return k <= 1 ? 0 : k + 2 * (k - 1);
   }
-  [[nodiscard]] rt::StreamHandle stream(std::size_t i) const { return streams_[i].native(); }
+  [[nodiscard]] rt::StreamHandle stream(std::size_t i) const { return lanes_[i].native(); }
 
  private:
   friend class GraphExecutor;
+  // One step of an iteration as the host issues it.  plan() compiles the whole
+  // iteration (fork, every node's waits / timing stamps / launch / record, join)
+  // into this list once; run_async() walks it.
+  struct Step {
+    enum class Kind : std::uint8_t { kWait, kRecord, kStampStart, kStampStop, kLaunch };
+    Kind kind = Kind::kLaunch;
+    std::uint16_t lane = 0;    // index into lanes_
+    std::uint32_t arg = 0;     // signal index (kWait, kRecord), scheduled node (the rest)
+  };
   std::vector<ScheduledNode> sched_;
   std::vector<std::uint32_t> wait_pool_;
-  std::vector<rt::Stream> streams_;
-  std::vector<rt::Event> events_;
-  std::vector<rt::Event> fork_event_;
-  std::vector<rt::Event> join_events_;
-  std::vector<rt::Event> probes_;
-  int probe_slots_ = 0;
-  int iteration_ = 0;
-  StreamAssignment streams_plan_;
-  MemoryPlan memory_plan_;
+  std::vector<rt::Stream> lanes_;
+  // Cross-stream events [0, E), then the fork event (E), then one join event per
+  // lane after the first (E + 1 ...).
+  std::vector<rt::Event> signals_;
+  std::vector<rt::Event> stamps_;   // timing stamps: (node * stamp_slots_ + slot) * 2 + {0 start, 1 stop}
+  std::vector<Step> program_;
+  int stamp_slots_ = 0;
+  int runs_ = 0;                     // iterations issued (selects the stamp slot and the poison pattern)
+  StreamAssignment schedule_;
+  MemoryPlan memory_;
   std::shared_ptr<Storage> arena_;
-  std::vector<std::shared_ptr<Storage>> workspaces_;
-  std::vector<std::pair<std::size_t, std::size_t>> input_byte_ranges_;
-  std::vector<std::vector<Tensor>> node_inputs_;
-  std::vector<std::vector<Tensor>> node_outputs_;
-  std::vector<Tensor> bound_;
-  std::shared_ptr<Storage> poison_src_;   // device-side pattern for poisoning
-  std::size_t peak_bytes_ = 0;
-  std::size_t naive_bytes_ = 0;
+  std::vector<std::shared_ptr<Storage>> lane_workspace_;
+  // Arena byte ranges that the poison fill rewrites each run: all but graph inputs.
+  std::vector<std::pair<std::size_t, std::size_t>> poison_ranges_;
+  std::vector<Tensor> bound_;                  // per tensor (undefined when unplaced)
+  std::vector<std::vector<Tensor>> reads_;     // per scheduled node
+  std::vector<std::vector<Tensor>> writes_;
+  std::size_t arena_bytes_ = 0;
+  std::size_t unshared_bytes_ = 0;
 };
 
 class GraphExecutor {
@@ -144,7 +155,7 @@ class GraphExecutor {
   // iteration's.  plan() drops the captured graph, since it binds the old plan's
   // buffers.
   [[nodiscard]] Status capture_graph();
-  [[nodiscard]] bool captured() const noexcept { return graph_exec_ != nullptr; }
+  [[nodiscard]] bool captured() const noexcept { return replay_ != nullptr; }
   [[nodiscard]] Status synchronize();
   [[nodiscard]] Status run_sync() {
     MCKE_RETURN_IF_ERROR(run_async());
@@ -161,14 +172,16 @@ class GraphExecutor {
   [[nodiscard]] ExecutorOptions& options() { return opts_; }
 
  private:
-  // Drains the plan's streams, returns its storages to the allocator while the
-  // streams they were last used on still exist, then drops the plan.
-  void release_plan();
-  [[nodiscard]] Status issue_plan();   // one iteration's launches, events and fills
-  [[nodiscard]] Status issue_poison(rt::Stream& s0);   // the poison fills of one iteration
-  [[nodiscard]] Status launch_node(std::size_t i, rt::Stream& st);   // scheduled node i's op
-  [[nodiscard]] Status assemble_across_streams(void** out_exec);
-  void release_capture();
+  // Waits for everything queued on the plan's streams, hands its storages back
+  // to the allocator while those streams still exist, and forgets the plan.
+  void drop_plan();
+  void drop_replay();
+  [[nodiscard]] Status run_program();                // one eager iteration
+  [[nodiscard]] Status refill_poison(rt::Stream& s0);
+  [[nodiscard]] Status launch(std::size_t i, rt::Stream& lane);   // scheduled node i's op
+  [[nodiscard]] Status capture_lanes(void** out_exec);            // multi-stream capture
+  struct GateOutcome;
+  [[nodiscard]] Status gate_config(SchedulePolicy sp, MemoryPolicy mp, int repeats, GateOutcome* out);
 
   Graph graph_;
   DeviceAllocator& alloc_;
@@ -177,12 +190,13 @@ class GraphExecutor {
   ExecutionPlan plan_;
   Profiler profiler_;
   std::vector<NodeTiming> node_timings_;
-  std::vector<std::pair<TensorId, std::vector<char>>> input_cache_;
+  // Host copies of the graph inputs, kept for validate_numerics() to replan with.
+  std::vector<std::pair<TensorId, std::vector<char>>> gate_inputs_;
   bool planned_ = false;
-  void* graph_exec_ = nullptr;   // hipGraphExec_t of the captured iteration
+  void* replay_ = nullptr;             // hipGraphExec_t of the captured iteration
   // hipGraph_t of each node's capture (multi-stream plans), kept until the
   // executable graph assembled from them is released.
-  std::vector<void*> capture_parts_;
+  std::vector<void*> replay_parts_;
 };
 
 }  // namespace mcke

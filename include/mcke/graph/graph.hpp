@@ -2,9 +2,9 @@
 //
 // Same API as the reference's include/mcke/graph/graph.hpp (and graph.cpp:59-441):
 // add_input / add_node (shapes inferred by the op) / mark_output / finalize
-// (consumers, preds and succs, a Kahn topological order that also detects cycles,
-// ASAP depth, ALAP depth and slack, and dead nodes that reach no output), plus
-// levels, live ranges over an order, the total ideal cost and a DOT dump.
+// (consumers, preds and succs, cycle detection, ASAP depth, ALAP depth and slack,
+// and dead nodes that reach no output), plus a topological order, levels, live
+// ranges over an order, the total ideal cost and a DOT dump.
 #pragma once
 
 #include <cassert>
@@ -91,7 +91,7 @@ class Graph {
   [[nodiscard]] std::vector<Shape> input_shapes(NodeId n) const;
 
  private:
-  [[nodiscard]] std::vector<NodeId> kahn_order() const;
+  [[nodiscard]] std::vector<NodeId> level_major_order() const;   // ASAP depth, then id
   [[nodiscard]] std::string describe(NodeId n) const;
   [[nodiscard]] std::string describe_tensor(TensorId t) const;
 

@@ -1,10 +1,11 @@
 // mcke/graph/memory_plan.hpp -- placement of every tensor in one arena.
 //
 // Same API as the reference's include/mcke/graph/memory_plan.hpp and
-// memory_plan.cpp:40-267.  Tensors are placed largest first (ties by id) at the
-// lowest 256-byte aligned offset that overlaps no already placed tensor it may
-// not share with.  Two tensors may share bytes when both are intermediates and,
-// under the policy, every access of one is ordered before the other's producer:
+// memory_plan.cpp:40-267.  Tensors are placed largest first (ties by id), each
+// in the smallest 256-byte aligned gap between the already placed tensors it may
+// not share with (or past them).  Two tensors may share bytes when both are
+// intermediates and, under the policy, every access of one is ordered before the
+// other's producer:
 //   kAllocPerTensor      never (the baseline);
 //   kReuseTopoNaive      by position in the topological order only -- UNSAFE
 //                        across streams, kept to show what the race check finds;

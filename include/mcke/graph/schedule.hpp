@@ -7,12 +7,13 @@
 //                   with a barrier between consecutive levels (the first node of
 //                   level d+1 on each stream waits for the last node of level d
 //                   on every other stream);
-//   kChainGreedy    a node with exactly one live predecessor whose stream has not
-//                   been continued yet inherits that stream; every other node goes
-//                   to the least-loaded stream (load = roofline time of its ideal
-//                   cost); every cross-stream predecessor becomes a wait.
-// Only producers that another stream waits on record an event, and each stream
-// waits on a given event at most once.
+//   kChainGreedy    a node whose only live predecessor has not passed its stream
+//                   on to another node yet inherits that stream; every other node
+//                   goes to the least-loaded stream (load = roofline time of its
+//                   ideal cost); every cross-stream predecessor must be ordered.
+// Cross-stream orderings become event waits, except where the waiting node's
+// vector clock already covers the producer (through its stream's earlier nodes
+// or an earlier wait); only producers left with a waiter record an event.
 #pragma once
 
 #include <cstdint>

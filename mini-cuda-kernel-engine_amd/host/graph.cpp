@@ -1,49 +1,70 @@
-// graph.cpp -- DAG construction, finalisation and queries
-// (reference src/graph/graph.cpp:59-441).
+// graph.cpp -- building a graph of ops over SSA tensors, finalising it, and the
+// queries the scheduler and memory planner use.
+//
+// Contract: reference include/mcke/graph/graph.hpp and src/graph/graph.cpp:59-441
+// (add_input / add_node with shape inference / mark_output / finalize; depths,
+// slack, dead nodes, levels, live ranges, total cost, DOT).  Structure here:
+//
+//   finalize()  wires consumers, predecessors (deduplicated, ascending) and
+//               successors; runs a three-colour depth-first search from every
+//               node that both finds a cycle (reported as the path around it)
+//               and yields a reverse postorder; computes ASAP depths along that
+//               order and heights against it; then marks liveness in one sweep
+//               from the sinks back (a node is live if it writes a graph output
+//               or feeds a live node).
+//   topological_order() is level-major: nodes by ASAP depth, then by id.  Every
+//               edge goes from a lower depth to a higher one, so this is a
+//               topological order, and it hands the scheduler each level's
+//               independent nodes together.
 #include "mcke/graph/graph.hpp"
 
 #include <algorithm>
-#include <deque>
 #include <limits>
+#include <numeric>
 #include <sstream>
 
 namespace mcke {
 
 namespace {
 
-Status check_shape(const Shape& s, const std::string& what) {
-  if (s.rank() < 1) return InvalidArgumentError(what + ": rank 0 (use rank 1 with dim 1 for a scalar)");
-  dim_t n = 1;
+Status validate_extents(const Shape& s, const std::string& who) {
+  if (s.rank() < 1)
+    return InvalidArgumentError(who + ": a tensor needs rank >= 1 (a scalar is shape {1})");
+  dim_t count = 1;
   for (int i = 0; i < s.rank(); ++i) {
     const dim_t d = s.dim(i);
-    if (d <= 0)
-      return InvalidArgumentError(what + ": dim " + std::to_string(i) + " is " + std::to_string(d) +
-                                  "; extents must be positive");
-    if (d > std::numeric_limits<dim_t>::max() / n)
-      return InvalidArgumentError(what + ": element count overflows int64");
-    n *= d;
+    if (d < 1) {
+      std::ostringstream os;
+      os << who << ": extent " << d << " in dimension " << i << " of " << s.to_string()
+         << " (extents start at 1)";
+      return InvalidArgumentError(os.str());
+    }
+    if (count > std::numeric_limits<dim_t>::max() / d)
+      return InvalidArgumentError(who + ": " + s.to_string() + " has more elements than int64 counts");
+    count *= d;
   }
-  if (!s.is_contiguous()) return InvalidArgumentError(what + ": strides are not row-major contiguous");
+  if (!s.is_contiguous())
+    return InvalidArgumentError(who + ": " + s.to_string() + " is strided; graph tensors are dense");
   return OkStatus();
 }
 
 }  // namespace
 
 std::string Graph::describe(NodeId n) const {
-  if (n >= nodes_.size()) return "node#" + std::to_string(n);
+  if (n >= nodes_.size()) return "<no node " + std::to_string(n) + ">";
   const Node& nd = nodes_[n];
-  return "node " + std::to_string(n) + " '" + nd.name + "' (" +
-         (nd.op ? std::string(nd.op->type_name()) : std::string("?")) + ")";
+  return "'" + nd.name + "' [" + (nd.op ? std::string(nd.op->type_name()) : std::string("no op")) +
+         " #" + std::to_string(n) + "]";
 }
 
 std::string Graph::describe_tensor(TensorId t) const {
-  if (t >= tensors_.size()) return "tensor#" + std::to_string(t);
-  return "tensor " + std::to_string(t) + " '" + tensors_[t].name + "' " + tensors_[t].shape.to_string();
+  if (t >= tensors_.size()) return "<no tensor " + std::to_string(t) + ">";
+  return "'" + tensors_[t].name + "' " + tensors_[t].shape.to_string() + " [#" + std::to_string(t) + "]";
 }
 
 StatusOr<TensorId> Graph::add_input(Shape shape, DType dtype, std::string name) {
-  if (finalized_) return FailedPreconditionError("add_input: graph is already finalized");
-  MCKE_RETURN_IF_ERROR(check_shape(shape, "add_input('" + name + "')"));
+  if (finalized_) return FailedPreconditionError("add_input: the graph is finalized; build a new one");
+  MCKE_RETURN_IF_ERROR(validate_extents(shape, "add_input '" + name + "'"));
   TensorDesc d;
   d.shape = shape;
   d.dtype = dtype;
@@ -54,228 +75,240 @@ StatusOr<TensorId> Graph::add_input(Shape shape, DType dtype, std::string name) 
 }
 
 StatusOr<std::vector<TensorId>> Graph::add_node(OpPtr op, std::vector<TensorId> inputs, std::string name) {
-  if (finalized_) return FailedPreconditionError("add_node: graph is already finalized");
-  if (!op) return InvalidArgumentError("add_node('" + name + "'): null op");
-  const std::string where = "add_node('" + name + "', " + std::string(op->type_name()) + ")";
-  std::vector<Shape> shapes;
-  shapes.reserve(inputs.size());
+  if (finalized_) return FailedPreconditionError("add_node: the graph is finalized; build a new one");
+  if (!op) return InvalidArgumentError("add_node '" + name + "': the op is null");
+  const std::string who = "add_node '" + name + "' (" + std::string(op->type_name()) + ")";
+  std::vector<Shape> in_shapes;
+  std::vector<DType> in_types;
   for (std::size_t i = 0; i < inputs.size(); ++i) {
-    if (inputs[i] >= tensors_.size())
-      return InvalidArgumentError(where + ": input " + std::to_string(i) + " is tensor " +
-                                  std::to_string(inputs[i]) + " but the graph has " +
-                                  std::to_string(tensors_.size()) + " tensors");
-    shapes.push_back(tensors_[inputs[i]].shape);
+    if (inputs[i] >= tensors_.size()) {
+      std::ostringstream os;
+      os << who << ": operand " << i << " names tensor " << inputs[i] << "; tensors 0.."
+         << tensors_.size() << " exist";
+      return InvalidArgumentError(os.str());
+    }
+    in_shapes.push_back(tensors_[inputs[i]].shape);
+    in_types.push_back(tensors_[inputs[i]].dtype);
   }
-  MCKE_ASSIGN_OR_RETURN(std::vector<Shape> outs, op->infer_shapes(shapes));
-  if (outs.empty()) return InvalidArgumentError(where + ": the op produced no outputs");
-  std::vector<DType> dtypes;
-  dtypes.reserve(inputs.size());
-  for (TensorId t : inputs) dtypes.push_back(tensors_[t].dtype);
-  auto out_dtype = op->infer_dtype(dtypes);
-  if (!out_dtype.ok())
-    return Status(out_dtype.status().code(), where + ": " + out_dtype.status().message());
-  const auto nid = static_cast<NodeId>(nodes_.size());
-  std::vector<TensorId> out_ids;
-  for (std::size_t k = 0; k < outs.size(); ++k) {
-    MCKE_RETURN_IF_ERROR(check_shape(outs[k], where + " output " + std::to_string(k)));
+  MCKE_ASSIGN_OR_RETURN(std::vector<Shape> out_shapes, op->infer_shapes(in_shapes));
+  if (out_shapes.empty()) return InvalidArgumentError(who + ": the op infers no outputs");
+  StatusOr<DType> out_type = op->infer_dtype(in_types);
+  if (!out_type.ok()) return Status(out_type.status().code(), who + ": " + out_type.status().message());
+  for (std::size_t k = 0; k < out_shapes.size(); ++k)
+    MCKE_RETURN_IF_ERROR(validate_extents(out_shapes[k], who + " result " + std::to_string(k)));
+
+  const auto id = static_cast<NodeId>(nodes_.size());
+  Node node;
+  node.op = std::move(op);
+  node.inputs = std::move(inputs);
+  node.name = name;
+  for (std::size_t k = 0; k < out_shapes.size(); ++k) {
     TensorDesc d;
-    d.shape = outs[k];
-    d.dtype = *out_dtype;
-    d.producer = nid;
-    d.name = outs.size() > 1 ? name + ":" + std::to_string(k) : name;
+    d.shape = out_shapes[k];
+    d.dtype = *out_type;
+    d.producer = id;
+    d.name = out_shapes.size() == 1 ? name : name + ":" + std::to_string(k);
+    node.outputs.push_back(static_cast<TensorId>(tensors_.size()));
     tensors_.push_back(std::move(d));
-    out_ids.push_back(static_cast<TensorId>(tensors_.size() - 1));
   }
-  Node n;
-  n.op = std::move(op);
-  n.inputs = std::move(inputs);
-  n.outputs = out_ids;
-  n.name = std::move(name);
-  nodes_.push_back(std::move(n));
-  return out_ids;
+  nodes_.push_back(std::move(node));
+  return nodes_.back().outputs;
 }
 
 Status Graph::mark_output(TensorId t) {
-  if (finalized_) return FailedPreconditionError("mark_output: graph is already finalized");
+  if (finalized_) return FailedPreconditionError("mark_output: the graph is finalized; build a new one");
   if (t >= tensors_.size())
-    return InvalidArgumentError("mark_output: tensor " + std::to_string(t) + " is out of range");
+    return InvalidArgumentError("mark_output: there is no tensor " + std::to_string(t));
   tensors_[t].is_graph_output = true;
   return OkStatus();
 }
 
-std::vector<NodeId> Graph::kahn_order() const {
-  std::vector<std::size_t> indeg(nodes_.size());
-  std::deque<NodeId> ready;
-  for (std::size_t n = 0; n < nodes_.size(); ++n) {
-    indeg[n] = nodes_[n].preds.size();
-    if (indeg[n] == 0) ready.push_back(static_cast<NodeId>(n));
-  }
-  std::vector<NodeId> order;
-  order.reserve(nodes_.size());
-  while (!ready.empty()) {
-    const NodeId n = ready.front();
-    ready.pop_front();
-    order.push_back(n);
-    for (NodeId s : nodes_[n].succs)
-      if (--indeg[s] == 0) ready.push_back(s);
-  }
-  return order;   // shorter than nodes_ means a cycle
+std::vector<NodeId> Graph::level_major_order() const {
+  std::vector<NodeId> order(nodes_.size());
+  std::iota(order.begin(), order.end(), 0u);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](NodeId a, NodeId b) { return nodes_[a].depth < nodes_[b].depth; });
+  return order;
 }
 
 Status Graph::finalize() {
   if (finalized_) return OkStatus();
-  if (nodes_.empty()) return FailedPreconditionError("finalize: graph has no nodes");
-  if (std::none_of(tensors_.begin(), tensors_.end(), [](const TensorDesc& t) { return t.is_graph_output; }))
-    return InvalidArgumentError("finalize: graph has no outputs; call mark_output()");
-  for (std::size_t n = 0; n < nodes_.size(); ++n)
-    for (std::size_t i = 0; i < nodes_[n].inputs.size(); ++i) {
-      const TensorDesc& d = tensors_[nodes_[n].inputs[i]];
-      if (d.producer == kInvalidNode && !d.is_graph_input)
-        return InvalidArgumentError("finalize: " + describe(static_cast<NodeId>(n)) + " input " +
-                                    std::to_string(i) + " has no producer and is not a graph input");
-    }
+  if (nodes_.empty()) return FailedPreconditionError("finalize: the graph has no nodes to run");
+  bool any_output = false;
+  for (const TensorDesc& d : tensors_) any_output = any_output || d.is_graph_output;
+  if (!any_output) return InvalidArgumentError("finalize: no tensor is marked as a graph output");
 
+  // Wiring.
   for (TensorDesc& d : tensors_) d.consumers.clear();
-  for (Node& nd : nodes_) {
+  for (std::size_t n = 0; n < nodes_.size(); ++n) {
+    Node& nd = nodes_[n];
     nd.preds.clear();
     nd.succs.clear();
-  }
-  for (std::size_t n = 0; n < nodes_.size(); ++n)
-    for (TensorId t : nodes_[n].inputs) tensors_[t].consumers.push_back(static_cast<NodeId>(n));
-  for (std::size_t n = 0; n < nodes_.size(); ++n) {
-    auto& p = nodes_[n].preds;
-    for (TensorId t : nodes_[n].inputs)
-      if (tensors_[t].producer != kInvalidNode) p.push_back(tensors_[t].producer);
-    std::sort(p.begin(), p.end());
-    p.erase(std::unique(p.begin(), p.end()), p.end());
+    for (std::size_t i = 0; i < nd.inputs.size(); ++i) {
+      TensorDesc& d = tensors_[nd.inputs[i]];
+      if (d.producer == kInvalidNode && !d.is_graph_input)
+        return InvalidArgumentError("finalize: " + describe(static_cast<NodeId>(n)) + " reads " +
+                                    describe_tensor(nd.inputs[i]) + ", which nothing produces");
+      d.consumers.push_back(static_cast<NodeId>(n));
+      if (d.producer != kInvalidNode) nd.preds.push_back(d.producer);
+    }
+    std::sort(nd.preds.begin(), nd.preds.end());
+    nd.preds.erase(std::unique(nd.preds.begin(), nd.preds.end()), nd.preds.end());
   }
   for (std::size_t n = 0; n < nodes_.size(); ++n)
     for (NodeId p : nodes_[n].preds) nodes_[p].succs.push_back(static_cast<NodeId>(n));
 
-  const std::vector<NodeId> order = kahn_order();
-  if (order.size() != nodes_.size()) {
-    std::vector<bool> placed(nodes_.size(), false);
-    for (NodeId n : order) placed[n] = true;
-    std::string cyc;
-    for (std::size_t n = 0; n < nodes_.size(); ++n)
-      if (!placed[n]) cyc += (cyc.empty() ? "" : ", ") + describe(static_cast<NodeId>(n));
-    return InternalError("finalize: graph has a cycle through [" + cyc + "]");
+  // Three-colour DFS over successor edges: a grey node met again closes a cycle.
+  enum : char { kWhite, kGrey, kBlack };
+  std::vector<char> colour(nodes_.size(), kWhite);
+  std::vector<NodeId> postorder;
+  postorder.reserve(nodes_.size());
+  std::vector<std::pair<NodeId, std::size_t>> path;   // node, next successor to try
+  for (std::size_t root = 0; root < nodes_.size(); ++root) {
+    if (colour[root] != kWhite) continue;
+    path.emplace_back(static_cast<NodeId>(root), 0);
+    colour[root] = kGrey;
+    while (!path.empty()) {
+      auto& [n, next] = path.back();
+      if (next == nodes_[n].succs.size()) {
+        colour[n] = kBlack;
+        postorder.push_back(n);
+        path.pop_back();
+        continue;
+      }
+      const NodeId s = nodes_[n].succs[next++];
+      if (colour[s] == kGrey) {
+        std::string ring;
+        bool on = false;
+        for (const auto& [m, unused] : path) {
+          (void)unused;
+          on = on || m == s;
+          if (on) ring += describe(m) + " -> ";
+        }
+        return InternalError("finalize: the graph has a cycle: " + ring + describe(s));
+      }
+      if (colour[s] == kWhite) {
+        colour[s] = kGrey;
+        path.emplace_back(s, 0);
+      }
+    }
   }
 
-  // ASAP depth, height, ALAP depth and slack.
-  for (Node& nd : nodes_) nd.depth = 0;
-  for (NodeId n : order)
-    for (NodeId p : nodes_[n].preds) nodes_[n].depth = std::max(nodes_[n].depth, nodes_[p].depth + 1);
-  int critical = 0;
-  for (const Node& nd : nodes_) critical = std::max(critical, nd.depth);
+  // Depths along the reverse postorder (a topological order), heights against it.
   std::vector<int> height(nodes_.size(), 0);
-  for (auto it = order.rbegin(); it != order.rend(); ++it)
-    for (NodeId s : nodes_[*it].succs) height[*it] = std::max(height[*it], height[s] + 1);
+  for (Node& nd : nodes_) nd.depth = 0;
+  for (auto it = postorder.rbegin(); it != postorder.rend(); ++it)
+    for (NodeId s : nodes_[*it].succs) nodes_[s].depth = std::max(nodes_[s].depth, nodes_[*it].depth + 1);
+  for (NodeId n : postorder)
+    for (NodeId s : nodes_[n].succs) height[n] = std::max(height[n], height[s] + 1);
+  int last_level = 0;
+  for (const Node& nd : nodes_) last_level = std::max(last_level, nd.depth);
   for (std::size_t n = 0; n < nodes_.size(); ++n) {
-    nodes_[n].alap_depth = critical - height[n];
+    nodes_[n].alap_depth = last_level - height[n];
     nodes_[n].slack = nodes_[n].alap_depth - nodes_[n].depth;
   }
 
-  // Dead nodes: those from which no graph output is reachable.
-  std::vector<bool> alive(nodes_.size(), false);
-  std::vector<NodeId> stack;
-  for (const TensorDesc& t : tensors_)
-    if (t.is_graph_output && t.producer != kInvalidNode && !alive[t.producer]) {
-      alive[t.producer] = true;
-      stack.push_back(t.producer);
-    }
-  while (!stack.empty()) {
-    const NodeId n = stack.back();
-    stack.pop_back();
-    for (NodeId p : nodes_[n].preds)
-      if (!alive[p]) {
-        alive[p] = true;
-        stack.push_back(p);
-      }
+  // Liveness: the postorder visits every node after all of its successors.
+  for (NodeId n : postorder) {
+    Node& nd = nodes_[n];
+    bool live = false;
+    for (TensorId t : nd.outputs) live = live || tensors_[t].is_graph_output;
+    for (NodeId s : nd.succs) live = live || !nodes_[s].is_dead;
+    nd.is_dead = !live;
   }
-  for (std::size_t n = 0; n < nodes_.size(); ++n) nodes_[n].is_dead = !alive[n];
   finalized_ = true;
   return OkStatus();
 }
 
 StatusOr<std::vector<NodeId>> Graph::topological_order() const {
-  if (!finalized_) return FailedPreconditionError("topological_order: call finalize() first");
-  return kahn_order();
+  if (!finalized_) return FailedPreconditionError("topological_order: finalize() the graph first");
+  return level_major_order();
 }
 
 StatusOr<std::vector<std::vector<NodeId>>> Graph::levels() const {
-  if (!finalized_) return FailedPreconditionError("levels: call finalize() first");
-  int critical = 0;
-  for (const Node& nd : nodes_) critical = std::max(critical, nd.depth);
-  std::vector<std::vector<NodeId>> out(static_cast<std::size_t>(critical) + 1);
-  for (std::size_t n = 0; n < nodes_.size(); ++n)
-    out[static_cast<std::size_t>(nodes_[n].depth)].push_back(static_cast<NodeId>(n));
-  return out;
+  if (!finalized_) return FailedPreconditionError("levels: finalize() the graph first");
+  std::vector<std::vector<NodeId>> by_depth;
+  for (NodeId n : level_major_order()) {
+    const auto d = static_cast<std::size_t>(nodes_[n].depth);
+    if (by_depth.size() <= d) by_depth.resize(d + 1);
+    by_depth[d].push_back(n);
+  }
+  return by_depth;
 }
 
 StatusOr<std::size_t> Graph::max_level_width() const {
-  MCKE_ASSIGN_OR_RETURN(std::vector<std::vector<NodeId>> lv, levels());
-  std::size_t w = 0;
-  for (const auto& l : lv) w = std::max(w, l.size());
-  return w;
+  MCKE_ASSIGN_OR_RETURN(std::vector<std::vector<NodeId>> by_depth, levels());
+  std::size_t widest = 0;
+  for (const auto& level : by_depth) widest = std::max(widest, level.size());
+  return widest;
 }
 
 std::vector<NodeId> Graph::dead_nodes() const {
-  std::vector<NodeId> out;
+  std::vector<NodeId> dead;
   for (std::size_t n = 0; n < nodes_.size(); ++n)
-    if (nodes_[n].is_dead) out.push_back(static_cast<NodeId>(n));
-  return out;
+    if (nodes_[n].is_dead) dead.push_back(static_cast<NodeId>(n));
+  return dead;
 }
 
+// def_pos: position of the producer in `order` (-1 for graph inputs); last_use_pos:
+// position of the last reader, order.size() for graph outputs, and never below def_pos.
 std::vector<Graph::LiveRange> Graph::compute_live_ranges(const std::vector<NodeId>& order) const {
-  std::vector<LiveRange> lr(tensors_.size());
-  for (std::size_t i = 0; i < order.size(); ++i) {
-    const NodeId n = order[i];
+  std::vector<LiveRange> ranges(tensors_.size());
+  for (int pos = 0; pos < static_cast<int>(order.size()); ++pos) {
+    const NodeId n = order[static_cast<std::size_t>(pos)];
     if (n >= nodes_.size()) continue;
     for (TensorId t : nodes_[n].outputs)
-      if (lr[t].def_pos < 0) lr[t].def_pos = static_cast<int>(i);
-    for (TensorId t : nodes_[n].inputs) lr[t].last_use_pos = std::max(lr[t].last_use_pos, static_cast<int>(i));
+      if (ranges[t].def_pos < 0) ranges[t].def_pos = pos;
+    for (TensorId t : nodes_[n].inputs) ranges[t].last_use_pos = std::max(ranges[t].last_use_pos, pos);
   }
   for (std::size_t t = 0; t < tensors_.size(); ++t) {
-    if (tensors_[t].is_graph_input) lr[t].def_pos = -1;
-    if (tensors_[t].is_graph_output) lr[t].last_use_pos = static_cast<int>(order.size());
-    if (lr[t].last_use_pos < lr[t].def_pos) lr[t].last_use_pos = lr[t].def_pos;
+    LiveRange& r = ranges[t];
+    if (tensors_[t].is_graph_input) r.def_pos = -1;
+    if (tensors_[t].is_graph_output) r.last_use_pos = static_cast<int>(order.size());
+    r.last_use_pos = std::max(r.last_use_pos, r.def_pos);
   }
-  return lr;
+  return ranges;
 }
 
 std::vector<Shape> Graph::input_shapes(NodeId n) const {
-  std::vector<Shape> in;
-  for (TensorId t : nodes_[n].inputs) in.push_back(tensors_[t].shape);
-  return in;
+  std::vector<Shape> shapes;
+  shapes.reserve(nodes_[n].inputs.size());
+  for (TensorId t : nodes_[n].inputs) shapes.push_back(tensors_[t].shape);
+  return shapes;
 }
 
 OpCost Graph::total_cost() const {
-  OpCost c;
-  for (std::size_t n = 0; n < nodes_.size(); ++n) {
-    if (!nodes_[n].op || nodes_[n].is_dead) continue;
-    const OpCost k = nodes_[n].op->cost(input_shapes(static_cast<NodeId>(n)));
-    c.flops += k.flops;
-    c.bytes += k.bytes;
-  }
-  return c;
-}
-
-std::string Graph::to_dot() const {
-  std::ostringstream os;
-  os << "digraph mcke {\n  rankdir=TB;\n";
-  for (std::size_t t = 0; t < tensors_.size(); ++t) {
-    const TensorDesc& d = tensors_[t];
-    os << "  t" << t << " [shape=box,label=\"" << d.name << "\\n" << d.shape.to_string() << "\""
-       << (d.is_graph_output ? ",style=bold" : "") << "];\n";
-  }
+  OpCost sum;
   for (std::size_t n = 0; n < nodes_.size(); ++n) {
     const Node& nd = nodes_[n];
-    os << "  n" << n << " [shape=ellipse,label=\"" << nd.name << "\\n"
+    if (nd.is_dead || !nd.op) continue;
+    const OpCost c = nd.op->cost(input_shapes(static_cast<NodeId>(n)));
+    sum.flops += c.flops;
+    sum.bytes += c.bytes;
+  }
+  return sum;
+}
+
+// Nodes as boxes, tensors as edges labelled with name and shape; graph inputs
+// come from one "inputs" point and graph outputs go to one "outputs" point.
+std::string Graph::to_dot() const {
+  std::ostringstream os;
+  os << "digraph G {\n  node [fontname=monospace];\n  inputs [shape=point];\n  outputs [shape=point];\n";
+  for (std::size_t n = 0; n < nodes_.size(); ++n) {
+    const Node& nd = nodes_[n];
+    os << "  op" << n << " [shape=box,label=\"" << nd.name << " : "
        << (nd.op ? std::string(nd.op->type_name()) : std::string("?")) << "\""
-       << (nd.is_dead ? ",style=dashed" : "") << "];\n";
-    for (TensorId t : nd.inputs) os << "  t" << t << " -> n" << n << ";\n";
-    for (TensorId t : nd.outputs) os << "  n" << n << " -> t" << t << ";\n";
+       << (nd.is_dead ? ",color=gray" : "") << "];\n";
+  }
+  auto edge = [&](const std::string& from, const std::string& to, TensorId t) {
+    os << "  " << from << " -> " << to << " [label=\"" << tensors_[t].name << " "
+       << tensors_[t].shape.to_string() << "\"];\n";
+  };
+  for (std::size_t t = 0; t < tensors_.size(); ++t) {
+    const TensorDesc& d = tensors_[t];
+    const std::string src = d.producer == kInvalidNode ? "inputs" : "op" + std::to_string(d.producer);
+    for (NodeId c : d.consumers) edge(src, "op" + std::to_string(c), static_cast<TensorId>(t));
+    if (d.is_graph_output) edge(src, "outputs", static_cast<TensorId>(t));
   }
   os << "}\n";
   return os.str();

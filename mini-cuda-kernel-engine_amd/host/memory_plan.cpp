@@ -1,5 +1,24 @@
-// memory_plan.cpp -- arena placement with happens-before sharing and the race
-// verifier (reference src/graph/memory_plan.cpp:40-267).
+// memory_plan.cpp -- every tensor of a schedule placed in one arena, and the
+// check that no two tensors sharing bytes can be live at the same time.
+//
+// Contract: reference include/mcke/graph/memory_plan.hpp and
+// src/graph/memory_plan.cpp:40-267 (four sharing policies, the MemoryPlan
+// record, verify_no_buffer_races).  Structure here:
+//
+//   * Lifetimes.  For each tensor: the scheduled index of its producer and of
+//     every node that reads it.  Tensor b may reuse tensor a's bytes when both
+//     are intermediates and every access of a is over before b's producer runs,
+//     where "over before" is the policy's notion: never (per-tensor), earlier in
+//     the issue order (topo-naive, which ignores streams and is unsafe -- kept to
+//     show what the race check catches), happens-before on one stream
+//     (same-stream), or happens-before across streams (happens-before).
+//   * Placement.  Largest tensors first (ties by id).  Each goes into the
+//     smallest gap between the already placed tensors it may not share with
+//     that holds it (best fit, gaps at 256-byte aligned offsets), or past the
+//     end of them when no gap does.  The arena is the highest end placed, so it
+//     never exceeds the sum of the sizes.
+//   * Race check.  The placed byte ranges are swept in offset order; every pair
+//     that overlaps must be ordered by happens-before, one way or the other.
 #include "mcke/graph/memory_plan.hpp"
 
 #include <algorithm>
@@ -9,157 +28,165 @@ namespace mcke {
 
 namespace {
 
-std::size_t align_up(std::size_t v, std::size_t a) { return (v + a - 1) / a * a; }
+constexpr std::uint32_t kNone = 0xFFFFFFFFu;
 
-const char* policy_name(MemoryPolicy p) {
-  switch (p) {
-    case MemoryPolicy::kAllocPerTensor: return "alloc_per_tensor";
-    case MemoryPolicy::kReuseTopoNaive: return "reuse_topo_naive(UNSAFE)";
-    case MemoryPolicy::kReuseSameStream: return "reuse_same_stream";
-    case MemoryPolicy::kReuseHappensBefore: return "reuse_happens_before";
-  }
-  return "?";
+std::size_t round_up(std::size_t v) {
+  return (v + kDeviceAlignment - 1) / kDeviceAlignment * kDeviceAlignment;
 }
 
-// Scheduled indices of the nodes touching each tensor (producer first).
-struct Uses {
-  std::uint32_t producer = kNoEventId;
-  std::vector<std::uint32_t> all;
+struct Lifetime {
+  std::uint32_t producer = kNone;        // scheduled index
+  std::vector<std::uint32_t> touches;    // producer (if scheduled) and readers
 };
 
-std::vector<Uses> collect_uses(const Graph& g, const std::vector<std::uint32_t>& idx_of) {
-  std::vector<Uses> u(g.num_tensors());
-  for (std::size_t t = 0; t < g.num_tensors(); ++t) {
+std::vector<Lifetime> lifetimes(const Graph& g, const StreamAssignment& sa) {
+  std::vector<std::uint32_t> at(g.num_nodes(), kNone);
+  for (std::size_t i = 0; i < sa.nodes.size(); ++i) at[sa.nodes[i]] = static_cast<std::uint32_t>(i);
+  std::vector<Lifetime> life(g.num_tensors());
+  for (std::size_t t = 0; t < life.size(); ++t) {
     const TensorDesc& d = g.tensor(static_cast<TensorId>(t));
-    if (d.producer != kInvalidNode && idx_of[d.producer] != kNoEventId) {
-      u[t].producer = idx_of[d.producer];
-      u[t].all.push_back(u[t].producer);
+    if (d.producer != kInvalidNode && at[d.producer] != kNone) {
+      life[t].producer = at[d.producer];
+      life[t].touches.push_back(life[t].producer);
     }
     for (NodeId c : d.consumers)
-      if (idx_of[c] != kNoEventId) u[t].all.push_back(idx_of[c]);
+      if (at[c] != kNone) life[t].touches.push_back(at[c]);
   }
-  return u;
+  return life;
+}
+
+// Is every access of tensor a over before tensor b is produced, under `policy`?
+bool over_before(MemoryPolicy policy, const Graph& g, const StreamAssignment& sa,
+                 const HappensBefore& hb, const std::vector<Lifetime>& life, TensorId a, TensorId b) {
+  if (policy == MemoryPolicy::kAllocPerTensor) return false;
+  if (!g.tensor(a).reusable() || !g.tensor(b).reusable()) return false;
+  const std::uint32_t pb = life[b].producer;
+  if (pb == kNone || life[a].touches.empty()) return false;
+  const auto& ta = life[a].touches;
+  switch (policy) {
+    case MemoryPolicy::kReuseTopoNaive:
+      return *std::max_element(ta.begin(), ta.end()) < pb;
+    case MemoryPolicy::kReuseSameStream:
+      return std::all_of(ta.begin(), ta.end(), [&](std::uint32_t u) {
+        return sa.stream_of[u] == sa.stream_of[pb] && hb.precedes(u, pb);
+      });
+    case MemoryPolicy::kReuseHappensBefore:
+      return std::all_of(ta.begin(), ta.end(), [&](std::uint32_t u) { return hb.precedes(u, pb); });
+    case MemoryPolicy::kAllocPerTensor:
+      break;
+  }
+  return false;
+}
+
+const char* policy_label(MemoryPolicy p) {
+  switch (p) {
+    case MemoryPolicy::kAllocPerTensor: return "one buffer per tensor";
+    case MemoryPolicy::kReuseTopoNaive: return "reuse by issue position (unsafe across streams)";
+    case MemoryPolicy::kReuseSameStream: return "reuse within a stream";
+    case MemoryPolicy::kReuseHappensBefore: return "reuse under happens-before";
+  }
+  return "?";
 }
 
 }  // namespace
 
 StatusOr<MemoryPlan> plan_memory(const Graph& g, const StreamAssignment& sa, const HappensBefore& hb,
                                  MemoryPolicy policy) {
+  const std::vector<Lifetime> life = lifetimes(g, sa);
   MemoryPlan mp;
   mp.policy = policy;
-  const std::size_t T = g.num_tensors();
-  mp.offset_of.assign(T, kNoOffset);
-  mp.bytes_of.assign(T, 0);
-  std::vector<std::uint32_t> idx_of(g.num_nodes(), kNoEventId);
-  for (std::size_t i = 0; i < sa.nodes.size(); ++i) idx_of[sa.nodes[i]] = static_cast<std::uint32_t>(i);
-  const std::vector<Uses> uses = collect_uses(g, idx_of);
+  mp.offset_of.assign(g.num_tensors(), kNoOffset);
+  mp.bytes_of.assign(g.num_tensors(), 0);
+
+  std::vector<TensorId> todo;
+  for (std::size_t t = 0; t < g.num_tensors(); ++t) {
+    const TensorDesc& d = g.tensor(static_cast<TensorId>(t));
+    const bool dead_producer = d.producer != kInvalidNode && life[t].producer == kNone;
+    const std::size_t bytes = round_up(d.shape.bytes(d.dtype));
+    if (dead_producer || bytes == 0) continue;
+    mp.bytes_of[t] = bytes;
+    mp.naive_bytes += bytes;
+    if (d.is_graph_input) mp.input_bytes += bytes;
+    else if (d.is_graph_output) mp.output_bytes += bytes;
+    else mp.intermediate_bytes += bytes;
+    todo.push_back(static_cast<TensorId>(t));
+  }
+  std::stable_sort(todo.begin(), todo.end(),
+                   [&](TensorId x, TensorId y) { return mp.bytes_of[x] > mp.bytes_of[y]; });
 
   std::vector<TensorId> placed;
-  for (std::size_t t = 0; t < T; ++t) {
-    const TensorDesc& d = g.tensor(static_cast<TensorId>(t));
-    if (d.producer != kInvalidNode && idx_of[d.producer] == kNoEventId) continue;   // dead producer
-    const std::size_t bytes = align_up(d.shape.bytes(d.dtype), kDeviceAlignment);
-    if (bytes == 0) continue;
-    mp.bytes_of[t] = bytes;
-    placed.push_back(static_cast<TensorId>(t));
-    (d.is_graph_input ? mp.input_bytes : d.is_graph_output ? mp.output_bytes : mp.intermediate_bytes) += bytes;
-    mp.naive_bytes += bytes;
-  }
-
-  // May tensor b take bytes that tensor a used?  Only if every use of a is over
-  // before b's producer starts.
-  auto a_before_b = [&](TensorId a, TensorId b) -> bool {
-    if (!g.tensor(a).reusable() || !g.tensor(b).reusable()) return false;
-    const std::uint32_t pb = uses[b].producer;
-    if (pb == kNoEventId || uses[a].all.empty()) return false;
-    switch (policy) {
-      case MemoryPolicy::kAllocPerTensor:
-        return false;
-      case MemoryPolicy::kReuseTopoNaive: {
-        std::uint32_t last = 0;
-        for (std::uint32_t n : uses[a].all) last = std::max(last, n);
-        return last < pb;
+  for (TensorId t : todo) {
+    const std::size_t need = mp.bytes_of[t];
+    // Byte ranges of the placed tensors t may not share with, in offset order.
+    std::vector<std::pair<std::size_t, std::size_t>> taken;
+    for (TensorId o : placed)
+      if (!over_before(policy, g, sa, hb, life, o, t) && !over_before(policy, g, sa, hb, life, t, o))
+        taken.emplace_back(mp.offset_of[o], mp.offset_of[o] + mp.bytes_of[o]);
+    std::sort(taken.begin(), taken.end());
+    std::size_t best = kNoOffset, best_gap = kNoOffset, cursor = 0;
+    for (const auto& [lo, hi] : taken) {
+      if (lo >= cursor && lo - cursor >= need && lo - cursor < best_gap) {
+        best = cursor;
+        best_gap = lo - cursor;
       }
-      case MemoryPolicy::kReuseSameStream:
-        for (std::uint32_t n : uses[a].all)
-          if (sa.stream_of[n] != sa.stream_of[pb] || !hb.precedes(n, pb)) return false;
-        return true;
-      case MemoryPolicy::kReuseHappensBefore:
-        for (std::uint32_t n : uses[a].all)
-          if (!hb.precedes(n, pb)) return false;
-        return true;
+      cursor = std::max(cursor, round_up(hi));
     }
-    return false;
-  };
-
-  std::vector<TensorId> by_size = placed;
-  std::sort(by_size.begin(), by_size.end(), [&](TensorId x, TensorId y) {
-    return mp.bytes_of[x] != mp.bytes_of[y] ? mp.bytes_of[x] > mp.bytes_of[y] : x < y;
-  });
-  std::vector<TensorId> done;
-  for (TensorId t : by_size) {
-    std::vector<std::pair<std::size_t, std::size_t>> busy;
-    for (TensorId u : done)
-      if (!a_before_b(u, t) && !a_before_b(t, u)) busy.emplace_back(mp.offset_of[u], mp.offset_of[u] + mp.bytes_of[u]);
-    std::sort(busy.begin(), busy.end());
-    std::size_t off = 0;
-    for (const auto& [lo, hi] : busy) {
-      if (off + mp.bytes_of[t] <= lo) break;
-      off = std::max(off, align_up(hi, kDeviceAlignment));
-    }
-    mp.offset_of[t] = off;
-    mp.arena_bytes = std::max(mp.arena_bytes, off + mp.bytes_of[t]);
-    done.push_back(t);
+    if (best == kNoOffset) best = cursor;   // past every conflicting tensor
+    mp.offset_of[t] = best;
+    mp.arena_bytes = std::max(mp.arena_bytes, best + need);
+    placed.push_back(t);
   }
-  std::vector<std::size_t> offs;
-  for (TensorId t : placed) offs.push_back(mp.offset_of[t]);
-  std::sort(offs.begin(), offs.end());
-  mp.buffers_used = static_cast<std::size_t>(std::unique(offs.begin(), offs.end()) - offs.begin());
 
+  std::vector<std::size_t> starts;
+  for (TensorId t : placed) starts.push_back(mp.offset_of[t]);
+  std::sort(starts.begin(), starts.end());
+  mp.buffers_used = static_cast<std::size_t>(std::unique(starts.begin(), starts.end()) - starts.begin());
+
+  // One workspace per stream, as large as the largest need of its nodes.
   mp.workspace_bytes.assign(sa.num_streams_used, 0);
-  for (std::size_t i = 0; i < sa.nodes.size(); ++i) {
-    const Node& nd = g.node(sa.nodes[i]);
-    if (!nd.op) continue;
-    const std::size_t w = nd.op->workspace_bytes(g.input_shapes(sa.nodes[i]));
-    auto& slot = mp.workspace_bytes[sa.stream_of[i]];
-    slot = std::max(slot, align_up(w, kDeviceAlignment));
-  }
+  for (std::size_t i = 0; i < sa.nodes.size(); ++i)
+    if (const Op* op = g.node(sa.nodes[i]).op.get()) {
+      std::size_t& w = mp.workspace_bytes[sa.stream_of[i]];
+      w = std::max(w, round_up(op->workspace_bytes(g.input_shapes(sa.nodes[i]))));
+    }
   return mp;
 }
 
 Status verify_no_buffer_races(const Graph& g, const StreamAssignment& sa, const HappensBefore& hb,
                               const MemoryPlan& mp) {
-  std::vector<std::uint32_t> idx_of(g.num_nodes(), kNoEventId);
-  for (std::size_t i = 0; i < sa.nodes.size(); ++i) idx_of[sa.nodes[i]] = static_cast<std::uint32_t>(i);
-  const std::vector<Uses> uses = collect_uses(g, idx_of);
-  // All uses of `a` precede the producer of `b`?
-  auto ordered = [&](std::size_t a, std::size_t b, std::uint32_t* bad_u, std::uint32_t* bad_v) {
-    const std::uint32_t pb = uses[b].producer;
-    if (pb == kNoEventId || uses[a].all.empty()) return false;
-    for (std::uint32_t u : uses[a].all)
+  const std::vector<Lifetime> life = lifetimes(g, sa);
+  // Is every access of `a` over before b's producer?  If not, *late is an access
+  // of `a` that is not (kNone when b has no producer or a no access at all).
+  auto finished_before = [&](std::size_t a, std::size_t b, std::uint32_t* late) -> bool {
+    *late = kNone;
+    const std::uint32_t pb = life[b].producer;
+    if (pb == kNone || life[a].touches.empty()) return false;
+    for (std::uint32_t u : life[a].touches)
       if (!hb.precedes(u, pb)) {
-        *bad_u = u;
-        *bad_v = pb;
+        *late = u;
         return false;
       }
     return true;
   };
-  const std::size_t T = g.num_tensors();
-  for (std::size_t a = 0; a < T; ++a) {
-    if (mp.offset_of[a] == kNoOffset) continue;
-    for (std::size_t b = a + 1; b < T; ++b) {
-      if (mp.offset_of[b] == kNoOffset) continue;
-      const std::size_t a0 = mp.offset_of[a], a1 = a0 + mp.bytes_of[a];
-      const std::size_t b0 = mp.offset_of[b], b1 = b0 + mp.bytes_of[b];
-      if (a1 <= b0 || b1 <= a0) continue;
-      std::uint32_t u = 0, v = 0;
-      if (ordered(a, b, &u, &v) || ordered(b, a, &u, &v)) continue;
+  std::vector<std::size_t> by_offset;
+  for (std::size_t t = 0; t < mp.offset_of.size(); ++t)
+    if (mp.offset_of[t] != kNoOffset) by_offset.push_back(t);
+  std::sort(by_offset.begin(), by_offset.end(),
+            [&](std::size_t x, std::size_t y) { return mp.offset_of[x] < mp.offset_of[y]; });
+  for (std::size_t i = 0; i < by_offset.size(); ++i) {
+    const std::size_t a = by_offset[i];
+    const std::size_t a_end = mp.offset_of[a] + mp.bytes_of[a];
+    for (std::size_t j = i + 1; j < by_offset.size() && mp.offset_of[by_offset[j]] < a_end; ++j) {
+      const std::size_t b = by_offset[j];
+      std::uint32_t ab = kNone, ba = kNone;
+      if (finished_before(a, b, &ab) || finished_before(b, a, &ba)) continue;
       std::ostringstream os;
-      os << "verify_no_buffer_races: tensors " << a << " ('" << g.tensor(static_cast<TensorId>(a)).name
-         << "') and " << b << " ('" << g.tensor(static_cast<TensorId>(b)).name << "') share bytes ["
-         << std::max(a0, b0) << "," << std::min(a1, b1) << ") but neither's uses are ordered before the "
-         << "other's producer";
-      if (u != v) os << "; " << hb.describe_pair(u, v);
+      os << "verify_no_buffer_races: '" << g.tensor(static_cast<TensorId>(a)).name << "' (tensor " << a
+         << ") and '" << g.tensor(static_cast<TensorId>(b)).name << "' (tensor " << b
+         << ") overlap at bytes [" << mp.offset_of[b] << ", "
+         << std::min(a_end, mp.offset_of[b] + mp.bytes_of[b]) << ") with neither finished before the other "
+         << "is written";
+      if (ab != kNone && ab != life[b].producer) os << "; " << hb.describe_pair(ab, life[b].producer);
       return InternalError(os.str());
     }
   }
@@ -168,14 +195,14 @@ Status verify_no_buffer_races(const Graph& g, const StreamAssignment& sa, const 
 
 std::string MemoryPlan::describe() const {
   std::ostringstream os;
-  os << "memory " << policy_name(policy) << ": arena " << arena_bytes << " B ("
-     << arena_bytes / 1048576.0 << " MiB) vs naive " << naive_bytes << " B (" << naive_bytes / 1048576.0
-     << " MiB)";
-  if (arena_bytes) os << "  ratio " << static_cast<double>(naive_bytes) / static_cast<double>(arena_bytes) << "x";
-  os << "\n  buffers " << buffers_used << "  inputs " << input_bytes << " B, intermediates "
-     << intermediate_bytes << " B, outputs " << output_bytes << " B\n";
+  os << "arena (" << policy_label(policy) << "): " << arena_bytes << " B in " << buffers_used
+     << " buffer(s), against " << naive_bytes << " B with no sharing";
+  if (arena_bytes) os << " (" << static_cast<double>(naive_bytes) / static_cast<double>(arena_bytes) << "x)";
+  os << "\n  graph inputs " << input_bytes << " B, intermediates " << intermediate_bytes
+     << " B, graph outputs " << output_bytes << " B";
   for (std::size_t s = 0; s < workspace_bytes.size(); ++s)
-    os << "  stream " << s << " workspace " << workspace_bytes[s] << " B\n";
+    if (workspace_bytes[s]) os << "\n  workspace s" << s << ": " << workspace_bytes[s] << " B";
+  os << "\n";
   return os.str();
 }
 

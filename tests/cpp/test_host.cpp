@@ -391,6 +391,40 @@ TEST(schedule_diamond_and_happens_before) {
   CHECK(!hb->precedes(3, 0));
 }
 
+TEST(schedule_prunes_waits_implied_by_clocks) {
+  // P, X from x; Q = P.X; R = ba(P); Z = P.Q.  Chain-greedy on 3 streams at
+  // 1 TFLOP/s: P -> s0, X -> s1, Q (two preds) -> s2 waiting on P and X, R (P's
+  // heir) -> s0, Z (two preds) -> the least-loaded s1.  Z needs P and Q; Q has
+  // already waited on P, so one wait (on Q) orders both: 4 cross-stream needs,
+  // 3 waits, 3 events (P, X, Q).
+  Graph g;
+  const TensorId x = *g.add_input(Shape{64, 64}, DType::kF32, "x");
+  const TensorId bi = *g.add_input(Shape{64}, DType::kF32, "b");
+  GemmParams gp;
+  gp.variant = K::GemmVariant::kMfmaF32;
+  gp.auto_tile = true;
+  const TensorId p = (*g.add_node(bias_act(), {x, bi}, "P"))[0];
+  const TensorId xx = (*g.add_node(bias_act(), {x, bi}, "X"))[0];
+  const TensorId q = (*g.add_node(std::make_unique<GemmOp>(gp), {p, xx}, "Q"))[0];
+  const TensorId r = (*g.add_node(bias_act(), {p, bi}, "R"))[0];
+  const TensorId z = (*g.add_node(std::make_unique<GemmOp>(gp), {p, q}, "Z"))[0];
+  CHECK_OK(g.mark_output(r));
+  CHECK_OK(g.mark_output(z));
+  CHECK_OK(g.finalize());
+  auto sa = plan_streams(g, SchedulePolicy::kChainGreedy, 3, Roofline{1.0, 8000.0});
+  CHECK(sa.ok());
+  // scheduled order P(0) X(1) Q(2) R(3) Z(4)
+  CHECK((sa->stream_of == std::vector<std::uint16_t>{0, 1, 2, 0, 1}));
+  CHECK_EQ(sa->waits_raw, std::size_t{4});
+  CHECK_EQ(sa->waits_dedup, std::size_t{3});
+  CHECK_EQ(sa->num_events, std::size_t{3});
+  CHECK_EQ(sa->waits_of[4].size(), std::size_t{1});
+  CHECK_EQ(sa->waits_of[4][0], sa->record_of[2]);
+  CHECK_OK(verify_plan_ordering(g, *sa));
+  auto hb = sa->happens_before();
+  CHECK(hb.ok() && hb->precedes(0, 4) && hb->precedes(2, 4) && hb->concurrent(3, 4));
+}
+
 TEST(happens_before_rejects_malformed) {
   // two nodes sharing an issue index on one stream
   CHECK(!HappensBefore::build(1, {0, 0}, {0, 0}, {kNoEventId, kNoEventId}, {{}, {}}, {0, 1}).ok());
