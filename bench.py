@@ -472,6 +472,256 @@ def gemm_sweep(m, stream, warm_ms=150.0, timed_ms=40.0):
     return out
 
 
+def ladder_section(m, stream, sm_count):
+    """Every variant the reference's own benches time, on MI355X, at BASELINE shapes:
+
+      gemm     every GemmVariant at 4096^3 with rocBLAS timed first and last
+               (bench/gemm_bench.cpp:565-573);
+      reduce   tree / shuffle x sum / max / mean and two-pass sum at 8192^2, and
+               shuffle vs two-pass at the starved 64 x 524288 (reduce_bench.cpp:225-240);
+      softmax  three-pass vs online at 32768 x {128, 1024, 4096}
+               (softmax_bench.cpp:220-223);
+      bias_act fused vs the unfused pair (bias_add + activation) for ReLU, GELU_tanh
+               and GELU_erf, the fusion ratio, the vector-width sweep at full and at
+               starved occupancy (one workgroup row per CU), and the cache-resident
+               512 x 512 control (bias_act_bench.cpp:261-311) at 16384 x 4096;
+      effective the two ~33.5 MB ops on one buffer set (the working set stays in the
+               256 MB Infinity Cache), beside their cold figure (rotating sets).
+
+    Memory-bound rows rotate over >= 768 MiB of buffers unless marked resident.
+    Returns (results, verify): verify(oracle) checks every row's output in the CPU
+    leg (GEMM rows by the 1024-entry spot check) and stores it under "parity"."""
+    D = m.DeviceBuffer
+    out, checks = {}, []
+
+    def timed(launch, warmup, iters, sets=1):
+        for i in range(warmup):
+            launch(i % sets)
+        e0, e1 = m.Event(), m.Event()
+        e0.record(stream)
+        for i in range(iters):
+            launch(i % sets)
+        e1.record(stream)
+        stream.synchronize()
+        return e0.elapsed_ms(e1) / iters
+
+    def hbm_row(name, ms, nbytes, **extra):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"name": name, "avg_ms": round(ms, 5), "gb_s": round(gbs, 1),
+                "frac": round(gbs / PEAK_HBM_GBS, 4), **extra}
+
+    # --- GEMM ladder at 4096^3 ------------------------------------------------
+    n = 4096
+    ha, hb = m.fill_random(n * n, 0x6E33A), m.fill_random(n * n, 0x8B10C)
+    a, b = D.from_array(ha), D.from_array(hb)
+    V, T = m.GemmVariant, m.GemmTile
+    ladder = [("naive_uncoalesced", V.kNaiveUncoalesced, T(), 1, 2),
+              ("naive", V.kNaive, T(), 1, 2),
+              ("tiled_smem_32", V.kTiledSmem, T(32, 32, 32, 1, 1), 2, 5),
+              ("tiled_regblock", V.kTiledRegBlock, T(128, 128, 8, 8, 8), 2, 5),
+              ("warp_tile_nodbuf", V.kWarpTileNoDbuf, T(128, 128, 8, 8, 8), 2, 5),
+              ("warp_tile", V.kWarpTile, T(128, 128, 8, 8, 8), 2, 5),
+              ("warp_tile_vec4", V.kWarpTileVec4, T(128, 128, 8, 8, 8), 2, 5),
+              ("mfma_f32", V.kMfmaF32, m.gemm_mfma_default_tile(n, n, n), 10, 20)]
+    rows = []
+
+    def gemm_row(label, variant, tile, warmup, iters):
+        c = D.zeros(n * n)
+        ms = timed(lambda _i: m.launch_gemm_f32(a, b, c, n, n, n, 1.0, 0.0, variant, tile,
+                                                stream).throw_if_error(), warmup, iters)
+        tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
+        row = {"name": label, "avg_ms": round(ms, 4), "tflops": round(tf, 3),
+               "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4)}
+        host_c = c.download(n * n, stream=stream)
+        checks.append(("gemm " + label, row, lambda orc, hc=host_c: spot(orc, hc)))
+        log(f"ladder gemm {label}: {ms:.3f} ms, {tf:.2f} TFLOP/s")
+        return row
+
+    def spot(orc, hc):
+        r = orc.spot_check_gemm(ha, hb, hc, n, n, n, 1.0, 1024, 0x5A11E, orc.tol_gemm(n),
+                                orc.abs_tol_gemm(n))
+        return {"ok": r.checked == 1024 and r.mismatches == 0, "max_abs_err": r.max_abs_err,
+                "check": "1024-entry spot check, rel tol_gemm + abs abs_tol_gemm"}
+
+    rows.append(gemm_row("rocblas_first", V.kCublasRef, None, 5, 20))
+    for label, variant, tile, w, it in ladder:
+        rows.append(gemm_row(label, variant, tile, w, it))
+    rows.append(gemm_row("rocblas_last", V.kCublasRef, None, 5, 20))
+    out["gemm_4096"] = rows
+    del a, b
+
+    # --- reduce ladder --------------------------------------------------------
+    RV = m.ReduceVariant
+    red = []
+    for (R, Cc, label) in ((8192, 8192, "8192x8192"), (64, 524288, "64x524288_starved")):
+        hx = m.fill_normal(R * Cc, 0x5EED12345)
+        sets = rotation_sets((R * Cc + R) * 4)
+        xs = [D.from_array(hx) for _ in range(sets)]
+        combos = ([(v, k) for v in (RV.kSmemTree, RV.kWarpShuffle) for k in (0, 1, 2)] +
+                  [(RV.kTwoPass, 0)]) if R == 8192 else [(RV.kWarpShuffle, 0), (RV.kTwoPass, 0)]
+        for var, kind in combos:
+            o = D(R * 4)
+            wsb = max(m.row_reduce_workspace_bytes(R, Cc, var), 4)
+            ws = D(wsb)
+            ms = timed(lambda i, var=var, kind=kind, o=o, ws=ws, wsb=wsb: m.launch_row_reduce_f32(
+                xs[i], o, R, Cc, kind, var, ws, wsb, stream).throw_if_error(), 3, 20, sets)
+            row = hbm_row(f"{var.name}_{['sum', 'max', 'mean'][kind]}_{label}", ms, (R * Cc + R) * 4)
+            got = o.download(R, stream=stream)
+
+            def check(orc, got=got, kind=kind, R=R, Cc=Cc, hx=hx):
+                want = orc.row_reduce(hx, R, Cc, kind)
+                if kind == 1:
+                    return {"ok": bool(np.array_equal(got, want)), "check": "max bit-exact"}
+                floor = 5e-5 * (1.0 / 0.577) * max(1.0, np.sqrt(Cc / 4096.0)) / (Cc if kind == 2 else 1)
+                r = orc.compare(got, want, 1e-5, floor)
+                return {"ok": bool(r.ok), "max_rel_err": r.max_rel_err,
+                        "check": f"rel 1e-5 + abs {floor:.3g}"}
+            checks.append(("reduce " + row["name"], row, check))
+            red.append(row)
+            log(f"ladder reduce {row['name']}: {ms * 1e3:.1f} us, {row['gb_s']} GB/s")
+        del xs
+    out["reduce"] = red
+
+    # --- softmax: three-pass vs online ------------------------------------------
+    SV = m.SoftmaxVariant
+    smx = []
+    for cols in (128, 1024, 4096):
+        R = 32768
+        hx = m.fill_normal(R * cols, 0x50F7A11 + cols, 0.0, 2.0)
+        sets = rotation_sets(2 * R * cols * 4)
+        xs, ys = [D.from_array(hx) for _ in range(sets)], [D(R * cols * 4) for _ in range(sets)]
+        for var in (SV.kThreePass, SV.kOnlineOnePass):
+            ms = timed(lambda i, var=var: m.launch_row_softmax_f32(xs[i], ys[i], R, cols, var,
+                                                                  stream).throw_if_error(),
+                       3, 20, sets)
+            row = hbm_row(f"{var.name}_32768x{cols}", ms, 2 * R * cols * 4)
+            got = ys[0].download(R * cols, stream=stream)
+            checks.append(("softmax " + row["name"], row,
+                           lambda orc, got=got, hx=hx, cols=cols: _abs_check(
+                               orc, got, orc.row_softmax(hx, 32768, cols), 1e-6)))
+            smx.append(row)
+            log(f"ladder softmax {row['name']}: {ms * 1e3:.1f} us, {row['gb_s']} GB/s")
+        del xs, ys
+    out["softmax"] = smx
+
+    # --- bias + activation ------------------------------------------------------
+    BR, BC = 16384, 4096
+    hxb = m.fill_normal(BR * BC, 0xB1A5AC7 + BR)
+    hbb = m.fill_random(BC, 0xB1A5B1A5, -0.5, 0.5)
+    sets = rotation_sets((2 * BR * BC + BC) * 4)
+    xs = [D.from_array(hxb) for _ in range(sets)]
+    bs = [D.from_array(hbb) for _ in range(sets)]
+    ys = [D(BR * BC * 4) for _ in range(sets)]
+    tmp = [D(BR * BC * 4) for _ in range(sets)]
+    fused_bytes, unfused_bytes = (2 * BR * BC + BC) * 4, (4 * BR * BC + BC) * 4
+    A = m.Activation
+    ba, results = [], {}
+
+    def fused(act, vw, max_rows=0):
+        return timed(lambda i: m.launch_bias_act_f32(xs[i], bs[i], ys[i], BR, BC, act, vw, stream,
+                                                     max_rows).throw_if_error(), 3, 20, sets)
+
+    def unfused(act, vw):
+        def pair(i):
+            m.launch_bias_add_f32(xs[i], bs[i], tmp[i], BR, BC, vw, stream).throw_if_error()
+            m.launch_activation_f32(tmp[i], ys[i], BR * BC, act, vw, stream).throw_if_error()
+        return timed(pair, 3, 20, sets)
+
+    for act in (A.kRelu, A.kGeluTanh, A.kGeluErf):
+        f_ms = fused(act, 4)
+        got_f = ys[0].download(BR * BC, stream=stream)
+        u_ms = unfused(act, 4)
+        got_u = ys[0].download(BR * BC, stream=stream)
+        row = hbm_row(f"fused_vw4_{act.name}", f_ms, fused_bytes,
+                      unfused_pair_ms=round(u_ms, 5), fusion_speedup=round(u_ms / f_ms, 3),
+                      unfused_pair_gb_s=round(unfused_bytes / (u_ms * 1e-3) / 1e9, 1))
+        checks.append(("bias_act " + row["name"], row,
+                       lambda orc, gf=got_f, gu=got_u, act=act: _bias_check(
+                           orc, gf, gu, hxb, hbb, BR, BC, int(act))))
+        results[int(act)] = got_f
+        ba.append(row)
+        log(f"ladder bias {row['name']}: {f_ms * 1e3:.1f} us fused, {u_ms * 1e3:.1f} us unfused "
+            f"({u_ms / f_ms:.2f}x)")
+    for vw in (1, 2, 4):
+        for label, max_rows in (("full", 0), ("starved", sm_count)):
+            ms = fused(A.kGeluTanh, vw, max_rows)
+            got = ys[0].download(BR * BC, stream=stream)
+            row = hbm_row(f"gelu_tanh_vw{vw}_{label}", ms, fused_bytes, max_row_blocks=max_rows)
+            checks.append(("bias_act " + row["name"], row,
+                           lambda orc, got=got: {"ok": bool(np.array_equal(
+                               got.view(np.uint32), results[int(A.kGeluTanh)].view(np.uint32))),
+                               "check": "bit-equal to the fused vw4 output"}))
+            ba.append(row)
+            log(f"ladder bias {row['name']}: {ms * 1e3:.1f} us, {row['gb_s']} GB/s")
+    del xs, bs, ys, tmp
+    # cache-resident control: 512 x 512, one buffer set
+    s = 512
+    cx, cb = D.from_array(hxb[:s * s]), D.from_array(hbb[:s])
+    cy, ct = D(s * s * 4), D(s * s * 4)
+    f_ms = timed(lambda _i: m.launch_bias_act_f32(cx, cb, cy, s, s, A.kGeluTanh, 4, stream,
+                                                  0).throw_if_error(), 10, 200)
+
+    def pair_small(_i):
+        m.launch_bias_add_f32(cx, cb, ct, s, s, 4, stream).throw_if_error()
+        m.launch_activation_f32(ct, cy, s * s, A.kGeluTanh, 4, stream).throw_if_error()
+    u_ms = timed(pair_small, 10, 200)
+    ba.append({"name": "gelu_tanh_512x512_resident", "avg_ms": round(f_ms, 5),
+               "unfused_pair_ms": round(u_ms, 5), "fusion_speedup": round(u_ms / f_ms, 3),
+               "note": "one buffer set: the working set stays in cache"})
+    out["bias_act"] = ba
+
+    # --- effective (cache-resident) figures of the two ~33.5 MB ops -------------
+    eff = []
+    R, cols = 32768, 128
+    hx = m.fill_normal(R * cols, 0x50F7A11 + cols, 0.0, 2.0)
+    x1, y1 = D.from_array(hx), D(R * cols * 4)
+    ms = timed(lambda _i: m.launch_row_softmax_f32(x1, y1, R, cols, SV.kOnlineOnePass,
+                                                  stream).throw_if_error(), 10, 200)
+    eff.append(hbm_row("softmax_c128_resident", ms, 2 * R * cols * 4))
+    br, bc = 4096, 1024
+    hx2, hb2 = m.fill_normal(br * bc, 0xB1A5AC7 + br), m.fill_random(bc, 0xB1A5B1A5, -0.5, 0.5)
+    x2, b2, y2 = D.from_array(hx2), D.from_array(hb2), D(br * bc * 4)
+    ms = timed(lambda _i: m.launch_bias_act_f32(x2, b2, y2, br, bc, A.kGeluTanh, 4, stream,
+                                                0).throw_if_error(), 10, 200)
+    eff.append(hbm_row("bias_gelu_4096x1024_resident", ms, (2 * br * bc + bc) * 4))
+    for e in eff:
+        log(f"ladder effective {e['name']}: {e['avg_ms'] * 1e3:.1f} us, {e['gb_s']} GB/s")
+    out["effective_resident"] = eff
+
+    def verify(orc):
+        ok = True
+        for label, row, check in checks:
+            row["parity"] = check(orc)
+            ok = ok and row["parity"]["ok"]
+            if not row["parity"]["ok"]:
+                log(f"ladder parity FAILED: {label}: {row['parity']}")
+        return {"ok": ok}
+
+    return out, verify
+
+
+def _abs_check(orc, got, want, tol):
+    r = orc.compare(got, want, 0.0, tol)
+    return {"ok": bool(r.ok), "max_abs_err": r.max_abs_err, "check": f"every element abs {tol:g}"}
+
+
+def _bias_check(orc, got_fused, got_unfused, hx, hb, rows, cols, act):
+    """The fused output and the unfused pair's, each against the CPU oracle at abs
+    1e-6 + rel 1e-6.  Where the fused kernel rounds v = x + b to f32 before the
+    activation (ReLU, GELU_tanh), as the pair's bias_add does, the two agree bit for
+    bit; the fused GELU_erf carries v exactly and may differ in the last bits."""
+    want = orc.bias_act(hx, hb, rows, cols, act)
+    rf = orc.compare(got_fused, want, 1e-6, 1e-6)
+    ru = orc.compare(got_unfused, want, 1e-6, 1e-6)
+    same = bool(np.array_equal(got_fused.view(np.uint32), got_unfused.view(np.uint32)))
+    need_same = act != 2
+    return {"ok": bool(rf.ok and ru.ok and (same or not need_same)),
+            "max_abs_err": rf.max_abs_err, "unfused_max_abs_err": ru.max_abs_err,
+            "unfused_same_bits": same,
+            "check": "fused and unfused pair: abs 1e-6 + rel 1e-6 against the CPU oracle; "
+                     "the same bits except for GELU_erf"}
+
+
 PEAK_16BIT_MFMA_TFLOPS = 2500.0   # MI355X dense bf16 / fp16 matrix, AMD published
 
 
@@ -1027,6 +1277,8 @@ def main(argv=None) -> int:
     p.add_argument("--no-graph", action="store_true", help="skip the config-5 graph section")
     p.add_argument("--no-peaks", action="store_true", help="skip the measured-peak microbenches")
     p.add_argument("--no-lp", action="store_true", help="skip the 16-bit-input GEMM section")
+    p.add_argument("--no-ladder", action="store_true",
+                   help="skip the variant ladder (every variant the reference's benches time)")
     p.add_argument("--only", default=None,
                    help="comma-separated op-name prefixes to run (profiling); enables "
                         "the copy_256mib calibration op")
@@ -1083,6 +1335,9 @@ def main(argv=None) -> int:
     graph_res, graph_verify = None, None
     if not (args.no_graph or only is not None):
         graph_res, graph_verify = graph_section(m)
+    ladder_res, ladder_verify = None, None
+    if not (args.no_ladder or only is not None):
+        ladder_res, ladder_verify = ladder_section(m, stream, info.sm_count)
     cpu = None
     if not args.no_cpu:
         # The CPU checker on every timed op's output at its timed shape (the timed
@@ -1097,6 +1352,8 @@ def main(argv=None) -> int:
         extra = list(lp_verify)
         if graph_verify is not None:
             extra.append(("graph (config 5 stages, timed-plan bits, numerics gates)", graph_verify))
+        if ladder_verify is not None:
+            extra.append(("ladder (every variant's output)", ladder_verify))
         for name, verify in extra:
             t0 = time.perf_counter()
             res = verify(oracle)
@@ -1146,6 +1403,7 @@ def main(argv=None) -> int:
         "gemm_sweep": sweep,
         "gemm_lp": lp_res,
         "graph": graph_res,
+        "ladder": ladder_res,
     }
     print(json.dumps(line), flush=True)
     del keep

@@ -3,18 +3,18 @@
 // Replaces kernels/bias_act.cu (launchers bias_act.cu:269-331, validation :208-229).
 // HBM-bound: 4 bytes in + 4 bytes out per element (+ the bias row once per
 // column strip).  The design for gfx950:
-//   * 256-thread workgroups (4 wave64s); thread t of column strip blockIdx.x owns
-//     VW consecutive columns, so a wave issues 64 x VW x 4 contiguous bytes
-//     (1 KiB at VW = 4: 16-byte global_load_dwordx4 per lane);
+//   * lane t of column strip blockIdx.x owns VW consecutive columns, so a wave
+//     issues 64 x VW x 4 contiguous bytes (1 KiB at VW = 4: a 16-byte
+//     global_load_dwordx4 per lane);
 //   * the bias vector for those columns is loaded once and kept in registers;
-//   * large launches: one workgroup row per matrix row, so every lane has one
-//     16-byte load in flight and the hardware streams workgroups through the CUs
-//     (rows beyond the grid's 65535 limit are walked with a stride of gridDim.y,
-//     four per iteration);
+//   * large launches: 1 KiB of a row per workgroup (one wave at VW = 4), one
+//     workgroup row per matrix row, so every lane has one vector load in flight and the hardware streams
+//     workgroups through the CUs (rows beyond the grid's 65535 limit are walked
+//     with a stride of gridDim.y, four per iteration);
 //   * small launches (at most two rounds of resident workgroups at one row each):
-//     each workgroup owns kChunkRows adjacent rows of its column strip and issues
-//     all their loads before any store, so the launch is one round of
-//     long-latency loads instead of two;
+//     256-lane workgroups that each own kChunkRows adjacent rows of their column
+//     strip and issue all their loads before any store, so the launch is one
+//     round of long-latency loads instead of two;
 //   * x and y are streamed with non-temporal loads/stores.
 #include <hip/hip_runtime.h>
 
@@ -27,18 +27,27 @@ namespace mcke_amd {
 namespace {
 
 constexpr int kThreads = 256;
+// Workgroups of the one-row-per-workgroup kernel move kRowBytes of a row: one
+// wave at VW = 4, 128 lanes at VW = 2, 256 at VW = 1.  The flat activation kernel
+// runs one-wave workgroups (kRowLanes).  On gfx950 one-wave workgroups each
+// moving one 16-byte vector per lane streamed a 2 x 256 MiB copy 3% faster than
+// 256-lane workgroups of the same shape (80.0 vs 82.5 us); workgroups moving less
+// than 1 KiB a row are slower again (GELU_tanh at 16384 x 4096 with one-wave
+// workgroups: 227 us at VW = 1, 124 us at VW = 2, 83 us at VW = 4).
+constexpr int kRowLanes = 64;
+constexpr int kRowBytes = 1024;
 constexpr int kRowUnroll = 4;
 constexpr int kChunkRows = 8;
 // At or below this many one-row workgroups a launch takes the chunked kernel.
 constexpr int64_t kChunkMaxBlocks = 4096;
 
-template <int VW, int ACT>
-__global__ __launch_bounds__(kThreads) void bias_act_kernel(const float* __restrict__ x,
-                                                            const float* __restrict__ bias,
-                                                            float* __restrict__ y,
-                                                            int64_t rows, int64_t cols_v) {
+template <int VW, int ACT, int NT>
+__global__ __launch_bounds__(NT) void bias_act_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ y, int64_t rows,
+                                                      int64_t cols_v) {
   using V = Vec<VW>;
-  const int64_t cv = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t cv = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
   if (cv >= cols_v) return;
   const V bv = reinterpret_cast<const V*>(bias)[cv];
   const V* __restrict__ xv = reinterpret_cast<const V*>(x) + cv;
@@ -104,16 +113,18 @@ __global__ __launch_bounds__(kThreads) void bias_act_chunk_kernel(const float* _
   }
 }
 
-// y = act(x) over a flat array (the unfused pair's second kernel).
+// y = act(x) over a flat array (the unfused pair's second kernel): one vector
+// per lane and one wave per workgroup over the whole array (the layout of the
+// fastest plain copy on gfx950); past the grid's limit lanes stride on.
 template <int VW, int ACT>
-__global__ __launch_bounds__(kThreads) void activation_kernel(const float* __restrict__ x,
-                                                              float* __restrict__ y,
-                                                              int64_t n_v) {
+__global__ __launch_bounds__(kRowLanes) void activation_kernel(const float* __restrict__ x,
+                                                               float* __restrict__ y,
+                                                               int64_t n_v) {
   using V = Vec<VW>;
   const V* __restrict__ xv = reinterpret_cast<const V*>(x);
   V* __restrict__ yv = reinterpret_cast<V*>(y);
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n_v;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kRowLanes;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kRowLanes + threadIdx.x; i < n_v;
        i += stride) {
     const V a = ld_stream(xv + i);
     V o;
@@ -167,8 +178,8 @@ int validate_2d(const char* who, const float* x, const float* y, int64_t rows, i
 // with a smaller grid measured 3-10% slower).  Capped at the hardware's 65535,
 // beyond which lanes walk the remaining rows kRowUnroll at a time, and at the
 // caller's max_row_blocks.
-dim3 grid_2d(int64_t rows, int64_t cols_v, int max_row_blocks, int rows_per_block = 1) {
-  const int64_t gx = (cols_v + kThreads - 1) / kThreads;
+dim3 grid_2d(int64_t rows, int64_t cols_v, int max_row_blocks, int lanes, int rows_per_block = 1) {
+  const int64_t gx = (cols_v + lanes - 1) / lanes;
   int64_t gy = (rows + rows_per_block - 1) / rows_per_block;
   if (gy > 65535) gy = 65535;
   if (max_row_blocks > 0 && gy > max_row_blocks) gy = max_row_blocks;
@@ -182,7 +193,7 @@ int launch_fused_vw(const float* x, const float* bias, float* y, int64_t rows, i
   const int64_t cols_v = cols / VW;
   const int64_t gx = (cols_v + kThreads - 1) / kThreads;
   if (gx * rows <= kChunkMaxBlocks) {
-    const dim3 grid = grid_2d(rows, cols_v, max_row_blocks, kChunkRows);
+    const dim3 grid = grid_2d(rows, cols_v, max_row_blocks, kThreads, kChunkRows);
 #define MCKE_CHUNK(A) bias_act_chunk_kernel<VW, A, kChunkRows><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v)
     switch (act) {
       case kActNone: MCKE_CHUNK(kActNone); break;
@@ -195,12 +206,13 @@ int launch_fused_vw(const float* x, const float* bias, float* y, int64_t rows, i
     MCKE_LAUNCH_CHECK("bias_act_chunk_kernel");
     return ok();
   }
-  const dim3 grid = grid_2d(rows, cols_v, max_row_blocks);
+  constexpr int L = kRowBytes / (4 * VW);
+  const dim3 grid = grid_2d(rows, cols_v, max_row_blocks, L);
   switch (act) {
-    case kActNone: bias_act_kernel<VW, kActNone><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v); break;
-    case kActRelu: bias_act_kernel<VW, kActRelu><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v); break;
-    case kActGeluErf: bias_act_kernel<VW, kActGeluErf><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v); break;
-    case kActGeluTanh: bias_act_kernel<VW, kActGeluTanh><<<grid, kThreads, 0, s>>>(x, bias, y, rows, cols_v); break;
+    case kActNone: bias_act_kernel<VW, kActNone, L><<<grid, L, 0, s>>>(x, bias, y, rows, cols_v); break;
+    case kActRelu: bias_act_kernel<VW, kActRelu, L><<<grid, L, 0, s>>>(x, bias, y, rows, cols_v); break;
+    case kActGeluErf: bias_act_kernel<VW, kActGeluErf, L><<<grid, L, 0, s>>>(x, bias, y, rows, cols_v); break;
+    case kActGeluTanh: bias_act_kernel<VW, kActGeluTanh, L><<<grid, L, 0, s>>>(x, bias, y, rows, cols_v); break;
     default: return invalid("launch_bias_act_f32: unknown activation " + std::to_string(act));
   }
   MCKE_LAUNCH_CHECK("bias_act_kernel");
@@ -210,14 +222,15 @@ int launch_fused_vw(const float* x, const float* bias, float* y, int64_t rows, i
 template <int VW>
 int launch_act_vw(const float* x, float* y, int64_t n, int act, hipStream_t s) {
   const int64_t n_v = n / VW;
-  int64_t blocks = (n_v + kThreads - 1) / kThreads;
-  if (blocks > 8192) blocks = 8192;
+  int64_t blocks = (n_v + kRowLanes - 1) / kRowLanes;
+  if (blocks > (1 << 30)) blocks = 1 << 30;
   const unsigned g = static_cast<unsigned>(blocks);
+  constexpr int L = kRowLanes;
   switch (act) {
-    case kActNone: activation_kernel<VW, kActNone><<<g, kThreads, 0, s>>>(x, y, n_v); break;
-    case kActRelu: activation_kernel<VW, kActRelu><<<g, kThreads, 0, s>>>(x, y, n_v); break;
-    case kActGeluErf: activation_kernel<VW, kActGeluErf><<<g, kThreads, 0, s>>>(x, y, n_v); break;
-    case kActGeluTanh: activation_kernel<VW, kActGeluTanh><<<g, kThreads, 0, s>>>(x, y, n_v); break;
+    case kActNone: activation_kernel<VW, kActNone><<<g, L, 0, s>>>(x, y, n_v); break;
+    case kActRelu: activation_kernel<VW, kActRelu><<<g, L, 0, s>>>(x, y, n_v); break;
+    case kActGeluErf: activation_kernel<VW, kActGeluErf><<<g, L, 0, s>>>(x, y, n_v); break;
+    case kActGeluTanh: activation_kernel<VW, kActGeluTanh><<<g, L, 0, s>>>(x, y, n_v); break;
     default: return invalid("launch_activation_f32: unknown activation " + std::to_string(act));
   }
   MCKE_LAUNCH_CHECK("activation_kernel");

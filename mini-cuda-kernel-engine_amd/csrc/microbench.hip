@@ -112,10 +112,13 @@ __global__ __launch_bounds__(kTriadThreads) void stream_triad_kernel(const float
 
 // The read+write ceiling for kernels that move one read and one write per
 // element (softmax, bias+act): y = x, one float4 per lane, non-temporal both
-// ways, one launch covering the array with no grid-stride loop.  Of the copy
-// shapes measured on MI355X (grid-stride loops at 256..16384 workgroups, 1..8
-// float4 per lane, plain or non-temporal accesses), this one moves the most.
-constexpr int kCopyThreads = 256;
+// ways, one launch covering the array with no grid-stride loop, one wave per
+// workgroup.  Of the copy shapes measured on MI355X (grid-stride loops at
+// 256..16384 workgroups with 1..8 float4 per lane, contiguous chunks per
+// workgroup, plain or non-temporal accesses, and this shape at 64..1024 lanes)
+// this one moves the most: 2 x 256 MiB in 80.0 us against 82.5 us with
+// 256-lane workgroups on the same box.
+constexpr int kCopyThreads = 64;
 
 __global__ __launch_bounds__(kCopyThreads) void stream_copy_kernel(const float* __restrict__ x,
                                                                    float* __restrict__ y,
