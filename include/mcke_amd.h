@@ -272,6 +272,9 @@ int mcke_rt_graph_add_child(void* graph, void* child, void* const* deps, size_t 
                             void** out_node);
 int mcke_rt_graph_instantiate(void* graph, void** out_exec);
 int mcke_rt_graph_release(void* graph);
+/* hipGraphUpload: moves an instantiated graph's launch resources to the device
+ * ahead of its first mcke_rt_graph_launch on `stream`. */
+int mcke_rt_graph_upload(void* exec, void* stream);
 
 /* raw_device_malloc / raw_device_free (device.cpp:104-130): hipMalloc, which is
  * 256-byte aligned; out-of-memory maps to MCKE_STATUS_OUT_OF_MEMORY. */

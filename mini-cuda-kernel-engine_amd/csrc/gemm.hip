@@ -247,6 +247,9 @@ struct MfmaCfg {
   int bm, bn, bk;
   MfmaFn even, vec, scalar;
   int even_threads;   // block size of `even` (the staged kernels use 256)
+  // Whole tiles when the launch is at most one round of workgroups (tiles <= CUs):
+  // a deeper stage ring for the same threads, or null to use `even`.
+  MfmaFn even_one_round = nullptr;
 };
 
 #define MCKE_MFMA_CFG(BM, BN, BK)                                                     \
@@ -259,20 +262,30 @@ struct MfmaCfg {
   {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST, KS>,                                \
    &gemm_mfma_kernel<BM, BN, 32, true, false>, &gemm_mfma_kernel<BM, BN, 32, false, false>, \
    kDmaThreads<BM, BN, KS>}
+#define MCKE_MFMA_CFG_DMA_ROUND(BM, BN, ST, KS, ST1)                                  \
+  {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST, KS>,                                \
+   &gemm_mfma_kernel<BM, BN, 32, true, false>, &gemm_mfma_kernel<BM, BN, 32, false, false>, \
+   kDmaThreads<BM, BN, KS>, &gemm_mfma_dma_kernel<BM, BN, ST1, KS>}
 
 // 64 x 64 tiles serve small problems, whose single round of tiles would leave
 // one wave per SIMD; two wave groups per tile measured 102.8 vs 89.9 TFLOP/s at
-// 1024^3 and 122.9 vs 120.4 at 2048^3.  For 128 x 128 they bought nothing
+// 1024^3 and 122.9 vs 120.4 at 2048^3.  With one workgroup per CU, a K step
+// (~1000 MFMA cycles) is short next to a load's round trip, so such a launch
+// takes a ring of 8 stages (128 KiB of LDS) instead of 4: 100.1-100.4 vs
+// 91.3-92.8 TFLOP/s at 1024^3 on one box, the same bits.  At more than one
+// round the 4-stage ring stays: it fits two workgroups per CU (2048^3 with 64 x
+// 64 tiles: 124.0 vs 114.8 TFLOP/s).  For 128 x 128 they bought nothing
 // (124.9 vs 124.7 at 2048^3, 130.6 vs 134.3 at 4096^3).  32 x 32 tiles (one wave
 // wide, four groups) give the smallest problems four times the workgroups of
 // 64 x 64: 40.0 vs 22.6 TFLOP/s at 512^3, 7.0 vs 4.5 at 256^3.
 const MfmaCfg kMfmaCfgs[] = {
     MCKE_MFMA_CFG_DMA(256, 256, 2, 1), MCKE_MFMA_CFG(256, 256, 16),
     MCKE_MFMA_CFG_DMA(128, 128, 2, 1), MCKE_MFMA_CFG(128, 128, 16),
-    MCKE_MFMA_CFG_DMA(64, 64, 4, 2),   MCKE_MFMA_CFG_DMA(32, 32, 4, 4),
+    MCKE_MFMA_CFG_DMA_ROUND(64, 64, 4, 2, 8), MCKE_MFMA_CFG_DMA(32, 32, 4, 4),
 };
 #undef MCKE_MFMA_CFG
 #undef MCKE_MFMA_CFG_DMA
+#undef MCKE_MFMA_CFG_DMA_ROUND
 
 const MfmaCfg* find_mfma(const mcke_gemm_tile& t) {
   for (const MfmaCfg& c : kMfmaCfgs)
@@ -285,7 +298,8 @@ struct Spec {
   GemmFn fn = nullptr;
   MfmaFn mfma = nullptr;
   MfmaFn mfma_even = nullptr;     // unchecked 16-byte variant for whole tiles
-  int even_threads = 0;           // its block size
+  MfmaFn mfma_even_one_round = nullptr;   // the same for at most one round of tiles
+  int even_threads = 0;           // their block size
   dim3 block{1, 1, 1};
   int threads = 0;                // block size of `kernel`
   int tile_m = 0, tile_n = 0, tile_k = 0;
@@ -345,6 +359,7 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
                        "(64,64,32,4,4) and (32,32,32,2,2); no fallback is applied");
       s.mfma = vec4 ? cfg->vec : cfg->scalar;
       s.mfma_even = vec4 ? cfg->even : nullptr;
+      s.mfma_even_one_round = vec4 ? cfg->even_one_round : nullptr;
       s.even_threads = cfg->even_threads;
       s.tile_k = cfg->bk;
       s.block = dim3(kMfmaThreads, 1, 1);
@@ -358,7 +373,9 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
     default:
       return invalid("launch_gemm_f32: unknown GemmVariant " + std::to_string(variant));
   }
-  // Attribute queries report the instantiation that whole-tile shapes run.
+  // Attribute queries report the instantiation that whole-tile shapes run (for a
+  // launch of at most one round of tiles the 64 x 64 tile runs a deeper stage
+  // ring of the same kernel: same lanes, more LDS).
   s.kernel = s.fn ? reinterpret_cast<const void*>(s.fn)
                   : reinterpret_cast<const void*>(s.mfma_even ? s.mfma_even : s.mfma);
   return ok();
@@ -437,7 +454,9 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
       return invalid("launch_gemm_f32: too many tiles for one launch");
     const bool whole = sp.mfma_even && m % sp.tile_m == 0 && n % sp.tile_n == 0 &&
                        k % sp.tile_k == 0;
-    const MfmaFn fn = whole ? sp.mfma_even : sp.mfma;
+    MfmaFn fn = whole ? sp.mfma_even : sp.mfma;
+    if (whole && sp.mfma_even_one_round && tiles_m * tiles_n <= device_cu_count())
+      fn = sp.mfma_even_one_round;
     const dim3 block = whole ? dim3(static_cast<unsigned>(sp.even_threads), 1, 1) : sp.block;
     fn<<<static_cast<unsigned>(tiles_m * tiles_n), block, 0, s>>>(
         a, b, c, mi, ni, ki, alpha, beta, static_cast<int>(tiles_m), static_cast<int>(tiles_n));

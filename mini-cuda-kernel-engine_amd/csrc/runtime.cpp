@@ -272,6 +272,12 @@ int mcke_rt_graph_instantiate(void* graph, void** out_exec) {
   return ok();
 }
 
+int mcke_rt_graph_upload(void* exec, void* stream) {
+  if (!exec) return invalid("mcke_rt_graph_upload: null graph");
+  MCKE_HIP_TRY(hipGraphUpload(static_cast<hipGraphExec_t>(exec), static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
 int mcke_rt_graph_release(void* graph) {
   if (!graph) return ok();
   MCKE_HIP_TRY(hipGraphDestroy(static_cast<hipGraph_t>(graph)));

@@ -312,7 +312,10 @@ Status GraphExecutor::capture_graph() {
     MCKE_RETURN_IF_ERROR(ended);
   }
   replay_ = exec;
-  return OkStatus();
+  // Stage the graph's launch resources now, not on the first replay.
+  MCKE_RETURN_IF_ERROR(from_abi(mcke_rt_graph_upload(replay_, plan_.lanes_.front().native()),
+                                "capture_graph: upload"));
+  return plan_.lanes_.front().synchronize();
 }
 
 // Several streams: no capture may span two of them, so each node's launches are
