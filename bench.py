@@ -857,8 +857,9 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
       * a 4x4 fan-out of 2048^3 GEMM chains on 4 streams (chain-greedy and
         level-parallel) vs the same graph on one stream, with the overlap (sum of
         node times / wall) and buddy statistics;
-      * the reference graph bench's diamond of 2048^3 GEMMs and its chain of 16
-        bias+GELU nodes on 4096x4096, under the three schedules;
+      * the reference graph bench's diamond of 2048^3 GEMMs, its chain of 16
+        bias+GELU nodes on 4096x4096 and its diamond of two grid-starved bias+GELU
+        nodes on 8192x4096, under the three schedules;
       * for every timed plan the launch-bound ratio (host enqueue time of one
         run / device time of one run, bench/graph_bench.cpp:437-441).
     At both config-5 shapes it also runs the numerics gate (3 schedules x 3 memory
@@ -1011,8 +1012,10 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
     out["fanout4x4_gemm2048"] = fan
 
     # The reference graph bench's other topologies (bench/graph_bench.cpp:100-166):
-    # a diamond of 2048^3 GEMMs (B and C from A, D from both) and a chain of 16
-    # bias+GELU nodes over X[4096 x 4096], each under the three schedules.
+    # a diamond of 2048^3 GEMMs (B and C from A, D from both), a chain of 16
+    # bias+GELU nodes over X[4096 x 4096], and a diamond whose two middle nodes
+    # are bias+GELU launches starved to 40 workgroup rows, each under the three
+    # schedules.
     def diamond_gemm(nn):
         g = G.Graph()
         a = g.add_input((nn, nn), "A")
@@ -1034,9 +1037,23 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
         return g, {"x": (x, m.fill_normal(rows * cols, 0x4300)),
                    "bias": (bias, m.fill_random(cols, 0x4301, -0.5, 0.5))}
 
+    def diamond_starved(rows, cols, blocks):
+        # B and C: bias+GELU nodes whose grids are capped at `blocks` workgroup rows
+        # (CU-idle but bandwidth-saturated); D joins B's output (graph_bench.cpp:138-153).
+        g = G.Graph()
+        x = g.add_input((rows, cols), "X")
+        bias = g.add_input((cols,), "bias")
+        left = g.add_bias_act(x, bias, "B_starved", act=3, max_row_blocks=blocks)
+        right = g.add_bias_act(x, bias, "C_starved", act=3, max_row_blocks=blocks)
+        g.mark_output(g.add_bias_act(left, bias, "D_join", act=3))
+        g.mark_output(right)
+        return g, {"X": (x, m.fill_normal(rows * cols, 0x4400)),
+                   "bias": (bias, m.fill_random(cols, 0x4401, -0.5, 0.5))}
+
     ref_graphs = {}
     for gname, build in (("diamond_gemm_2048", lambda: diamond_gemm(2048)),
-                         ("chain16_4096x4096", lambda: chain16(4096, 4096))):
+                         ("chain16_4096x4096", lambda: chain16(4096, 4096)),
+                         ("diamond_starved_8192x4096_40", lambda: diamond_starved(8192, 4096, 40))):
         rows = {}
         for label, sched, streams in (("sequential", G.SchedulePolicy.kSequential, 1),
                                       ("level_parallel", G.SchedulePolicy.kLevelParallel, 4),

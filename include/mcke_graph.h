@@ -105,6 +105,12 @@ int mcke_graph_add_gemm(mcke_graph* g, uint32_t a, uint32_t b, float alpha, int 
                         const mcke_gemm_tile* tile, const char* name, uint32_t* out_tensor);
 int mcke_graph_add_bias_act(mcke_graph* g, uint32_t x, uint32_t bias, int act, int vector_width,
                             const char* name, uint32_t* out_tensor);
+/* The same node with BiasActParams::max_row_blocks (reference op.hpp BiasActParams,
+ * ops_bias_act.cpp:102-130): caps the row dimension of the launch grid (0 =
+ * automatic), as the reference graph bench's starved diamond uses. */
+int mcke_graph_add_bias_act_rows(mcke_graph* g, uint32_t x, uint32_t bias, int act,
+                                 int vector_width, int max_row_blocks, const char* name,
+                                 uint32_t* out_tensor);
 int mcke_graph_add_reduce(mcke_graph* g, uint32_t x, int kind, int variant, const char* name,
                           uint32_t* out_tensor);
 int mcke_graph_add_softmax(mcke_graph* g, uint32_t x, int variant, const char* name, uint32_t* out_tensor);

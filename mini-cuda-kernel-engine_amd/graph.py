@@ -97,6 +97,8 @@ def host_lib() -> C.CDLL:
         "mcke_graph_add_gemm": (C.c_int, [_VP, _U32, _U32, C.c_float, C.c_int, C.POINTER(GemmTile),
                                           C.c_char_p, _U32P]),
         "mcke_graph_add_bias_act": (C.c_int, [_VP, _U32, _U32, C.c_int, C.c_int, C.c_char_p, _U32P]),
+        "mcke_graph_add_bias_act_rows": (C.c_int, [_VP, _U32, _U32, C.c_int, C.c_int, C.c_int,
+                                                   C.c_char_p, _U32P]),
         "mcke_graph_add_reduce": (C.c_int, [_VP, _U32, C.c_int, C.c_int, C.c_char_p, _U32P]),
         "mcke_graph_add_softmax": (C.c_int, [_VP, _U32, C.c_int, C.c_char_p, _U32P]),
         "mcke_graph_mark_output": (C.c_int, [_VP, _U32]),
@@ -183,10 +185,13 @@ class Graph:
         return self._out(host_lib().mcke_graph_add_gemm(self.h, a, b, alpha, int(variant), tp,
                                                         name.encode(), C.byref(out)), out)
 
-    def add_bias_act(self, x: int, bias: int, name: str, act=3, vector_width: int = 0) -> int:
+    def add_bias_act(self, x: int, bias: int, name: str, act=3, vector_width: int = 0,
+                     max_row_blocks: int = 0) -> int:
+        """max_row_blocks caps the launch grid's row dimension (0 = automatic)."""
         out = C.c_uint32()
-        return self._out(host_lib().mcke_graph_add_bias_act(self.h, x, bias, int(act), vector_width,
-                                                            name.encode(), C.byref(out)), out)
+        return self._out(host_lib().mcke_graph_add_bias_act_rows(
+            self.h, x, bias, int(act), vector_width, max_row_blocks, name.encode(),
+            C.byref(out)), out)
 
     def add_reduce(self, x: int, name: str, kind=0, variant=1) -> int:
         out = C.c_uint32()

@@ -106,13 +106,21 @@ int mcke_graph_add_gemm(mcke_graph* g, uint32_t a, uint32_t b, float alpha, int 
   return add_op<mcke::GemmOp>(g, std::make_unique<mcke::GemmOp>(p), {a, b}, name, out);
 }
 
-int mcke_graph_add_bias_act(mcke_graph* g, uint32_t x, uint32_t bias, int act, int vector_width,
-                            const char* name, uint32_t* out) {
+int mcke_graph_add_bias_act_rows(mcke_graph* g, uint32_t x, uint32_t bias, int act,
+                                 int vector_width, int max_row_blocks, const char* name,
+                                 uint32_t* out) {
   if (act < 0 || act > 3) return bad("mcke_graph_add_bias_act: unknown activation");
+  if (max_row_blocks < 0) return bad("mcke_graph_add_bias_act: negative max_row_blocks");
   mcke::BiasActParams p;
   p.act = static_cast<mcke::BiasActParams::Act>(act);
   p.vector_width = vector_width;
+  p.max_row_blocks = max_row_blocks;
   return add_op<mcke::BiasActOp>(g, std::make_unique<mcke::BiasActOp>(p), {x, bias}, name, out);
+}
+
+int mcke_graph_add_bias_act(mcke_graph* g, uint32_t x, uint32_t bias, int act, int vector_width,
+                            const char* name, uint32_t* out) {
+  return mcke_graph_add_bias_act_rows(g, x, bias, act, vector_width, 0, name, out);
 }
 
 int mcke_graph_add_reduce(mcke_graph* g, uint32_t x, int kind, int variant, const char* name, uint32_t* out) {

@@ -131,6 +131,44 @@ def test_gemm_fanout_streams_and_parity(G, orc):
     assert {x["stream"] for x in tim} == {0, 1, 2, 3}
 
 
+def test_starved_bias_act_diamond(G, orc):
+    """The reference graph bench's starved diamond (graph_bench.cpp:138-153): two
+    bias+GELU nodes whose grids are capped at a few workgroup rows and a join on
+    the first.  Every output against the CPU oracle, and the same bits for caps of
+    3 and 40 rows as without a cap (0)."""
+    rows, cols = 1000, 512
+    x = orc.fill_normal(rows * cols, 0x4400)
+    b = orc.fill_random(cols, 0x4401, -0.5, 0.5)
+    h = orc.bias_act(x, b, rows, cols, 3)
+    seen = []
+    for blocks in (0, 3, 40):
+        g = G.Graph()
+        tx = g.add_input((rows, cols), "X")
+        tb = g.add_input((cols,), "bias")
+        left = g.add_bias_act(tx, tb, "B_starved", act=3, max_row_blocks=blocks)
+        right = g.add_bias_act(tx, tb, "C_starved", act=3, max_row_blocks=blocks)
+        join = g.add_bias_act(left, tb, "D_join", act=3)
+        g.mark_output(join)
+        g.mark_output(right)
+        ex = G.Executor(g, schedule=G.SchedulePolicy.kLevelParallel, num_streams=2)
+        try:
+            ex.plan()
+            ex.set_input(tx, x)
+            ex.set_input(tb, b)
+            ex.run_sync()
+            got_r = ex.read(right, rows * cols)
+            got_d = ex.read(join, rows * cols)
+        finally:
+            ex.close()
+        r = orc.compare(got_r, h, 1e-6, 1e-6)
+        assert r.ok, f"cap {blocks}: {r}"
+        # the join reads B's output, which C's output equals bit for bit
+        r = orc.compare(got_d, orc.bias_act(got_r, b, rows, cols, 3), 1e-6, 1e-6)
+        assert r.ok, f"cap {blocks}: {r}"
+        seen.append(np.concatenate([got_r, got_d]).view(np.uint32))
+    assert all(np.array_equal(seen[0], s_) for s_ in seen[1:])
+
+
 def test_level_parallel_event_counts(G):
     g, _ = G.gemm_fanout(4, 4, 64)
     ex = G.Executor(g, schedule=G.SchedulePolicy.kLevelParallel, num_streams=4)
