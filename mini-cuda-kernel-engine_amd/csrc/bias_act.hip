@@ -27,8 +27,8 @@ namespace mcke_amd {
 namespace {
 
 constexpr int kThreads = 256;
-// Workgroups of the one-row-per-workgroup kernel move kRowBytes of a row: one
-// wave at VW = 4, 128 lanes at VW = 2, 256 at VW = 1.  The flat activation kernel
+// Workgroups of the row kernel move kRowBytes of a row: one wave at VW = 4, 128
+// lanes at VW = 2, 256 at VW = 1, each workgroup over 4 / VW rows at once.  The flat activation kernel
 // runs one-wave workgroups (kRowLanes).  On gfx950 one-wave workgroups each
 // moving one 16-byte vector per lane streamed a 2 x 256 MiB copy 3% faster than
 // 256-lane workgroups of the same shape (80.0 vs 82.5 us); workgroups moving less
@@ -207,7 +207,9 @@ int launch_fused_vw(const float* x, const float* bias, float* y, int64_t rows, i
     return ok();
   }
   constexpr int L = kRowBytes / (4 * VW);
-  const dim3 grid = grid_2d(rows, cols_v, max_row_blocks, L);
+  // Below VW = 4 each workgroup takes 4 / VW rows at once (the kernel's unrolled
+  // row walk), so a lane still has 16 bytes of loads in flight.
+  const dim3 grid = grid_2d(rows, cols_v, max_row_blocks, L, 4 / VW);
   switch (act) {
     case kActNone: bias_act_kernel<VW, kActNone, L><<<grid, L, 0, s>>>(x, bias, y, rows, cols_v); break;
     case kActRelu: bias_act_kernel<VW, kActRelu, L><<<grid, L, 0, s>>>(x, bias, y, rows, cols_v); break;

@@ -78,7 +78,7 @@ template <int WIDTH = 64> __device__ __forceinline__ float wave_max(float v) {
 // happens:
 //   GELU_erf(v) = 0.5 v (1 + erf(v / sqrt 2)) = 0.5 v erfc(-v / sqrt 2)
 //     v >= 0 :  y = vh + (vl - 0.5 vh erfc(v / sqrt 2))
-//     v <  0 :  y = 0.5 (vh + vl) erfc(-v / sqrt 2)
+//     v <  0 :  y = 0.5 vh erfc(-v / sqrt 2)
 // ---------------------------------------------------------------------------
 enum : int { kActNone = 0, kActRelu = 1, kActGeluErf = 2, kActGeluTanh = 3 };
 
@@ -106,16 +106,30 @@ __device__ __forceinline__ float gelu_tanh_xb(float x, float b) {
   return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a));
 }
 
+// erfc(s) for s >= 0 by Abramowitz & Stegun 7.1.26 (Hastings' approximation):
+// t = 1 / (1 + p s), erfc(s) ~= t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-s^2),
+// absolute error <= 1.5e-7 in exact arithmetic.  Branch-free: one reciprocal,
+// five FMAs and one base-2 exponential, where the library erfcf branches over
+// several ranges.  In GELU_erf on float inputs, evaluated in f32 with the
+// hardware exponential and reciprocal each one ulp off, the error stays within
+// 0.22 of abs 1e-6 + rel 1e-6 against the double formula over |v| <= 14.
+__device__ __forceinline__ float erfc_nonneg(float s) {
+  constexpr float kLog2eF = 1.4426950408889634f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, s, 1.0f));
+  float p = 1.061405429f;
+  p = __builtin_fmaf(p, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.254829592f);
+  return (p * t) * __builtin_amdgcn_exp2f(-(s * s) * kLog2eF);
+}
+
 __device__ __forceinline__ float gelu_erf_xb(float x, float b) {
   float v, vl;
   two_sum(x, b, v, vl);
-  const float t = v * 0.70710678118654752440f;
-  float y;
-  if (v >= 0.0f) {
-    y = v + __builtin_fmaf(-0.5f * v, erfcf(t), vl);
-  } else {
-    y = 0.5f * erfcf(-t) * (v + vl);
-  }
+  const float e = erfc_nonneg(__builtin_fabsf(v) * 0.70710678118654752440f);
+  const float half = 0.5f * v;
+  float y = (v >= 0.0f) ? v + __builtin_fmaf(-half, e, vl) : half * e;
   if (__builtin_isinf(v)) y = (v > 0.0f) ? v : __builtin_nanf("");
   return y;
 }

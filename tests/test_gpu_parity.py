@@ -118,6 +118,29 @@ def test_bias_act_width_invariance_and_starved_grid(gpu, orc):
 
 
 @pytest.mark.parametrize("act", [0, 1, 2, 3])
+def test_activation_special_values(gpu, orc, act):
+    """Infinities, NaN, signed zeros, tiny and huge magnitudes, through the fused
+    kernel with a zero bias and through the unfused activation kernel: the same
+    values as the double-precision reference (reference.hpp:116-136 evaluated on
+    x + b): NaN where it gives NaN (GELU of -inf is -inf * 0), +-inf where it
+    gives +-inf, and finite values within abs 1e-6 + rel 1e-6."""
+    vals = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 1e-30, -1e-30, 1e-7, -1e-7, 3.0, -3.0,
+                     9.5, -9.5, 30.0, -30.0, 88.0, -88.0, 1e3, -1e3, 1e30, -1e30, 3e38, -3e38,
+                     0.5, -0.5, 6.0, -6.0, 12.0, -12.0, 1.0, -1.0, 2.0], np.float32)
+    n = vals.size
+    want = orc.bias_act(vals, np.zeros(n, np.float32), 1, n, act)
+    for got in (run_bias_act(gpu, vals, np.zeros(n, np.float32), 1, n, act, 4),
+                run_activation(gpu, vals, n, act, 4)):
+        nan_w, nan_g = np.isnan(want), np.isnan(got)
+        assert np.array_equal(nan_w, nan_g), (vals[nan_w != nan_g], got[nan_w != nan_g])
+        fin = ~nan_w
+        inf_w = np.isinf(want[fin])
+        assert np.array_equal(got[fin][inf_w], want[fin][inf_w])
+        r = orc.compare(got[fin][~inf_w], want[fin][~inf_w], 1e-6, 1e-6)
+        assert r.ok, f"act {act}: {r}"
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
 def test_activation_unfused(gpu, orc, act):
     n = 3 * 4096
     x = orc.fill_normal(n, 11, 0.0, 3.0)
