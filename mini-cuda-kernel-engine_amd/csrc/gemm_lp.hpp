@@ -440,6 +440,20 @@ __device__ __forceinline__ void lds_wait(u32x4 (&av)[MT], u32x2 (&bv)[NT][2]) {
   }
 }
 
+// One global_load_lds_dwordx4 in its SGPR-base form: lane l's 16 bytes at
+// base + voff + OFF land at LDS byte m0 + OFF + 16 l (the immediate offset applies
+// to both addresses, so consecutive instructions of a stage share one M0).  The
+// 64-bit base is wave-uniform and the per-lane offset 32-bit: the 64-bit
+// per-lane address of the generic form cost a 64-bit VALU add and a
+// v_readfirstlane for M0 per instruction, and those, issued between the MFMAs,
+// held back the matrix pipe (measured: 1345 vs 1215 cycles per K step at
+// 8192^3, bf16).  The s_nop covers an M0 write just before the instruction.
+template <int OFF>
+__device__ __forceinline__ void lds_dma16(uint32_t voff, const void* base, uint32_t m0) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 offset:%2"
+               :: "v"(voff), "s"(base), "i"(OFF), "{m0}"(m0) : "memory");
+}
+
 template <int BM, int BN, int STAGES>
 struct LpDmaShape {
   static constexpr int BK = 32;
@@ -462,20 +476,24 @@ struct LpDmaShape {
   static_assert(STAGES >= 3 && (STAGES - 2) * L <= 63, "vmcnt counts at most 63 loads");
   static_assert(STAGES * kStageBytes <= 160 * 1024, "LDS holds 160 KiB");
   static_assert((16 + 4) * kBRow + 4 * 32 * kARow < 65536, "ds offsets are 16-bit");
+  static_assert(NA <= 4 && NB <= 4, "DMA immediate offsets stay below 4 KiB");
 
-  // Issues DMA instruction ii (A chunks first, then B) of this wave's share of
-  // K step `kstep` into the stage at `stage`.
-  static __device__ __forceinline__ void issue_dma(int ii, const char* a_base, const char* b_base,
+  // Issues DMA instruction II (A chunks first, then B) of this wave's share of
+  // K step `kstep` into the stage at LDS address `stage`.  a_src / b_src are the
+  // per-lane source offsets less the instruction's immediate offset (II * 1024
+  // within its operand), `wave` the wave index as a uniform value.
+  template <int II>
+  static __device__ __forceinline__ void issue_dma(const char* a_base, const char* b_base,
                                                    int64_t b_step, const uint32_t (&a_src)[NA],
                                                    const uint32_t (&b_src)[NB], int kstep,
-                                                   char* stage, int wave) {
-    if (ii < NA) {
-      __builtin_amdgcn_global_load_lds(a_base + static_cast<int64_t>(kstep) * (BK * 2) + a_src[ii],
-                                       stage + (wave * NA + ii) * 1024, 16, 0, 0);
+                                                   uint32_t stage, uint32_t wave) {
+    if constexpr (II < NA) {
+      lds_dma16<II * 1024>(a_src[II], a_base + static_cast<int64_t>(kstep) * (BK * 2),
+                           stage + wave * (NA * 1024));
     } else {
-      const int ib = ii - NA;
-      __builtin_amdgcn_global_load_lds(b_base + kstep * b_step + b_src[ib],
-                                       stage + kABytes + (wave * NB + ib) * 1024, 16, 0, 0);
+      constexpr int IB = II - NA;
+      lds_dma16<IB * 1024>(b_src[IB], b_base + kstep * b_step,
+                           stage + kABytes + wave * (NB * 1024));
     }
   }
 
@@ -508,7 +526,7 @@ __device__ __forceinline__ void lp_dma_slot(f32x16 (&acc)[BM / 64][BN / 64],
                                             bool dma, const char* a_base, const char* b_base,
                                             int64_t b_step, const uint32_t (&a_src)[LpDmaShape<BM, BN, STAGES>::NA],
                                             const uint32_t (&b_src)[LpDmaShape<BM, BN, STAGES>::NB],
-                                            int kstep, char* dstage, int wave) {
+                                            int kstep, uint32_t dstage, uint32_t wave) {
   using S = LpDmaShape<BM, BN, STAGES>;
   constexpr int i = IDX / S::NT, j = IDX % S::NT;
   const u32x4 b = u32x4{cbv[j][0][0], cbv[j][0][1], cbv[j][1][0], cbv[j][1][1]};
@@ -524,10 +542,12 @@ __device__ __forceinline__ void lp_dma_slot(f32x16 (&acc)[BM / 64][BN / 64],
      ...);
   }(std::make_integer_sequence<int, S::kReads>{});
   if (dma) {
-#pragma unroll
-    for (int ii = 0; ii < S::L; ++ii)
-      if (ii * S::kMfmas / S::L == IDX)
-        S::issue_dma(ii, a_base, b_base, b_step, a_src, b_src, kstep, dstage, wave);
+    [&]<int... II>(std::integer_sequence<int, II...>) {
+      ((II * S::kMfmas / S::L == IDX
+            ? S::template issue_dma<II>(a_base, b_base, b_step, a_src, b_src, kstep, dstage, wave)
+            : void()),
+       ...);
+    }(std::make_integer_sequence<int, S::L>{});
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -597,19 +617,25 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
   const char* a_base = reinterpret_cast<const char*>(A + static_cast<int64_t>(m0) * K);
   const char* b_base = reinterpret_cast<const char*>(B + n0);
   const int64_t b_step = static_cast<int64_t>(BK) * N * 2;        // bytes per stage
+  // Less the immediate offset of instruction ii (ii * 1024), which the DMA adds to
+  // both addresses; row >= 16 ii (A) and >= kBRowsPerChunk ii with N >= BN (B) keep
+  // the difference non-negative.
   uint32_t a_src[S::NA], b_src[S::NB];
 #pragma unroll
   for (int ii = 0; ii < S::NA; ++ii) {
     const int row = 16 * (wave * S::NA + ii) + lane / 4;       // (row / 4) % 4 == lane / 16
     const int q = (lane % 4) ^ (lane / 16);
-    a_src[ii] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) * 2u + 16u * q;
+    a_src[ii] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) * 2u + 16u * q -
+                1024u * ii;
   }
 #pragma unroll
   for (int ii = 0; ii < S::NB; ++ii) {
     const int row = S::kBRowsPerChunk * (wave * S::NB + ii) + lane / S::kBChunksPerRow;
     const int cg = (lane % S::kBChunksPerRow) ^ (4 * (row % 4));
-    b_src[ii] = static_cast<uint32_t>(row) * static_cast<uint32_t>(N) * 2u + 16u * cg;
+    b_src[ii] = static_cast<uint32_t>(row) * static_cast<uint32_t>(N) * 2u + 16u * cg -
+                1024u * ii;
   }
+  const uint32_t wave_u = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(wave));
 
   // Fragment addressing (bytes within a stage).
   //   A, m-tile i, sub-step s: row wm*WM + 32 i + c, chunk 2 s + h at position
@@ -645,11 +671,14 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
     // re-fetches the last one into a buffer nobody reads, which keeps the number
     // of loads per stage -- and so the vmcnt arithmetic -- uniform).
 #pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st)
-#pragma unroll
-      for (int ii = 0; ii < L; ++ii)
-        S::issue_dma(ii, a_base, b_base, b_step, a_src, b_src, st < ksteps ? st : ksteps - 1,
-                     smem + st * S::kStageBytes, wave);
+    for (int st = 0; st < STAGES - 1; ++st) {
+      const int kst = st < ksteps ? st : ksteps - 1;
+      [&]<int... II>(std::integer_sequence<int, II...>) {
+        (S::template issue_dma<II>(a_base, b_base, b_step, a_src, b_src, kst,
+                                   lds0 + st * S::kStageBytes, wave_u),
+         ...);
+      }(std::make_integer_sequence<int, L>{});
+    }
     asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - 2) * L) : "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -663,7 +692,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
     const uint32_t st_next = lds0 + ((ks + 1) % STAGES) * S::kStageBytes;
     const int kf = ks + STAGES - 1;
     const int kdma = kf < ksteps ? kf : ksteps - 1;
-    char* dstage = smem + (kf % STAGES) * S::kStageBytes;
+    const uint32_t dstage = lds0 + (kf % STAGES) * S::kStageBytes;
 
     // Sub-step 0 (fragments read in the previous step or the prologue).
     lds_wait<MT, NT>(av0, bv0);
@@ -671,7 +700,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
     [&]<int... I>(std::integer_sequence<int, I...>) {
       (lp_dma_slot<T, TRANS, BM, BN, STAGES, 1, I>(acc, av0, bv0, st, a_off, b_off, av1, bv1, false,
                                             a_base, b_base, b_step, a_src, b_src, kdma, dstage,
-                                            wave),
+                                            wave_u),
        ...);
     }(std::make_integer_sequence<int, S::kMfmas>{});
 
@@ -692,7 +721,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
     [&]<int... I>(std::integer_sequence<int, I...>) {
       (lp_dma_slot<T, TRANS, BM, BN, STAGES, 0, I>(acc, av1, bv1, st_next, a_off, b_off, av0, bv0,
                                             true, a_base, b_base, b_step, a_src, b_src, kdma,
-                                            dstage, wave),
+                                            dstage, wave_u),
        ...);
     }(std::make_integer_sequence<int, S::kMfmas>{});
   }
