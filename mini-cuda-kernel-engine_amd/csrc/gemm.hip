@@ -250,6 +250,9 @@ struct MfmaCfg {
   // Whole tiles when the launch is at most one round of workgroups (tiles <= CUs):
   // a deeper stage ring for the same threads, or null to use `even`.
   MfmaFn even_one_round = nullptr;
+  // `even` is the direct-to-LDS kernel, whose per-lane source offsets are 32-bit
+  // byte offsets within a tile's BM rows of A and 32 rows of B.
+  bool even_dma = false;
 };
 
 #define MCKE_MFMA_CFG(BM, BN, BK)                                                     \
@@ -261,11 +264,11 @@ struct MfmaCfg {
 #define MCKE_MFMA_CFG_DMA(BM, BN, ST, KS)                                             \
   {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST, KS>,                                \
    &gemm_mfma_kernel<BM, BN, 32, true, false>, &gemm_mfma_kernel<BM, BN, 32, false, false>, \
-   kDmaThreads<BM, BN, KS>}
+   kDmaThreads<BM, BN, KS>, nullptr, true}
 #define MCKE_MFMA_CFG_DMA_ROUND(BM, BN, ST, KS, ST1)                                  \
   {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST, KS>,                                \
    &gemm_mfma_kernel<BM, BN, 32, true, false>, &gemm_mfma_kernel<BM, BN, 32, false, false>, \
-   kDmaThreads<BM, BN, KS>, &gemm_mfma_dma_kernel<BM, BN, ST1, KS>}
+   kDmaThreads<BM, BN, KS>, &gemm_mfma_dma_kernel<BM, BN, ST1, KS>, true}
 
 // 64 x 64 tiles serve small problems, whose single round of tiles would leave
 // one wave per SIMD; two wave groups per tile measured 102.8 vs 89.9 TFLOP/s at
@@ -300,6 +303,7 @@ struct Spec {
   MfmaFn mfma_even = nullptr;     // unchecked 16-byte variant for whole tiles
   MfmaFn mfma_even_one_round = nullptr;   // the same for at most one round of tiles
   int even_threads = 0;           // their block size
+  bool even_dma = false;          // they take 32-bit per-lane source offsets
   dim3 block{1, 1, 1};
   int threads = 0;                // block size of `kernel`
   int tile_m = 0, tile_n = 0, tile_k = 0;
@@ -361,6 +365,7 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
       s.mfma_even = vec4 ? cfg->even : nullptr;
       s.mfma_even_one_round = vec4 ? cfg->even_one_round : nullptr;
       s.even_threads = cfg->even_threads;
+      s.even_dma = cfg->even_dma;
       s.tile_k = cfg->bk;
       s.block = dim3(kMfmaThreads, 1, 1);
       s.threads = s.mfma_even ? cfg->even_threads : kMfmaThreads;
@@ -453,7 +458,9 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
     if (tiles_m * tiles_n > 2147483647LL)
       return invalid("launch_gemm_f32: too many tiles for one launch");
     const bool whole = sp.mfma_even && m % sp.tile_m == 0 && n % sp.tile_n == 0 &&
-                       k % sp.tile_k == 0;
+                       k % sp.tile_k == 0 &&
+                       (!sp.even_dma || (static_cast<int64_t>(sp.tile_m) * k < (int64_t{1} << 30) &&
+                                         static_cast<int64_t>(32) * n < (int64_t{1} << 30)));
     MfmaFn fn = whole ? sp.mfma_even : sp.mfma;
     if (whole && sp.mfma_even_one_round && tiles_m * tiles_n <= device_cu_count())
       fn = sp.mfma_even_one_round;

@@ -440,20 +440,6 @@ __device__ __forceinline__ void lds_wait(u32x4 (&av)[MT], u32x2 (&bv)[NT][2]) {
   }
 }
 
-// One global_load_lds_dwordx4 in its SGPR-base form: lane l's 16 bytes at
-// base + voff + OFF land at LDS byte m0 + OFF + 16 l (the immediate offset applies
-// to both addresses, so consecutive instructions of a stage share one M0).  The
-// 64-bit base is wave-uniform and the per-lane offset 32-bit: the 64-bit
-// per-lane address of the generic form cost a 64-bit VALU add and a
-// v_readfirstlane for M0 per instruction, and those, issued between the MFMAs,
-// held back the matrix pipe (measured: 1345 vs 1215 cycles per K step at
-// 8192^3, bf16).  The s_nop covers an M0 write just before the instruction.
-template <int OFF>
-__device__ __forceinline__ void lds_dma16(uint32_t voff, const void* base, uint32_t m0) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 offset:%2"
-               :: "v"(voff), "s"(base), "i"(OFF), "{m0}"(m0) : "memory");
-}
-
 template <int BM, int BN, int STAGES>
 struct LpDmaShape {
   static constexpr int BK = 32;

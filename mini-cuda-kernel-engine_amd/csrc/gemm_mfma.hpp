@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <utility>
 
 #include "device_math.hpp"
 
@@ -453,18 +454,39 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
 //     consecutive rows; the swizzle puts any 8 (or 16) consecutive rows of a slot
 //     on distinct 16-byte bank groups, so they are conflict-free without padding.
 // ---------------------------------------------------------------------------
-// Issues direct-to-LDS instruction i of a wave's share of one stage (A chunks
+// One global_load_lds_dwordx4 in its SGPR-base form: lane l's 16 bytes at
+// base + voff + OFF land at LDS byte m0 + OFF + 16 l (the immediate offset applies
+// to both addresses, so up to four consecutive 1 KB chunks share one M0).  The
+// 64-bit base is wave-uniform and the per-lane offset 32-bit: the generic form's
+// 64-bit per-lane address cost a 64-bit VALU add and a v_readfirstlane for M0
+// per instruction, issued between the MFMAs (16-bit GEMM, 8192^3 bf16: 1345 vs
+// 1215 cycles per K step).  The s_nop covers an M0 write just before the
+// instruction.
+template <int OFF>
+__device__ __forceinline__ void lds_dma16(uint32_t voff, const void* base, uint32_t m0) {
+  static_assert(OFF >= 0 && OFF < 4096, "immediate offsets are 12-bit here");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 offset:%2"
+               :: "v"(voff), "s"(base), "i"(OFF), "{m0}"(m0) : "memory");
+}
+
+// Issues direct-to-LDS instruction I of a wave's share of one stage (A chunks
 // first, then B chunks) for K columns [k0, k0 + 32): 16 bytes per lane into the
-// wave-uniform 1 KB chunk of `stage` that the instruction owns.
-__device__ __forceinline__ void mfma_dma_issue(int i, int na, int nb, int a_floats,
-                                               const float* const* srcA, const float* const* srcB,
-                                               int64_t stepB, float* stage, int k0, int wave) {
-  if (i < na) {
-    __builtin_amdgcn_global_load_lds(srcA[i] + k0, stage + (wave * na + i) * 256, 16, 0, 0);
+// 1 KB chunk of the stage at LDS address `stage` that the instruction owns.
+// offA / offB are the lanes' byte offsets from a_base / b_base for k0 = 0, less
+// the instruction's immediate offset ((I % 4) KB within its operand); `wave` is
+// the wave index as a uniform value.
+template <int I, int NA, int NB>
+__device__ __forceinline__ void mfma_dma_issue(int a_floats, const uint32_t (&offA)[NA],
+                                               const uint32_t (&offB)[NB], const char* a_base,
+                                               const char* b_base, int64_t stepB_bytes,
+                                               uint32_t stage, int k0, uint32_t wave) {
+  if constexpr (I < NA) {
+    lds_dma16<(I % 4) * 1024>(offA[I], a_base + static_cast<int64_t>(k0) * 4,
+                              stage + (wave * NA + (I & ~3)) * 1024);
   } else {
-    const int ib = i - na;
-    __builtin_amdgcn_global_load_lds(srcB[ib] + static_cast<int64_t>(k0 / 32) * stepB,
-                                     stage + a_floats + (wave * nb + ib) * 256, 16, 0, 0);
+    constexpr int IB = I - NA;
+    lds_dma16<(IB % 4) * 1024>(offB[IB], b_base + static_cast<int64_t>(k0 / 32) * stepB_bytes,
+                               stage + a_floats * 4 + (wave * NB + (IB & ~3)) * 1024);
   }
 }
 
@@ -518,24 +540,33 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
   const int wm = wg / WGN, wn = wg % WGN;
   const int h = lane / 32, c = lane % 32;
 
-  // This lane's source addresses for its wave's chunks of stage 0 (advanced by BK
-  // columns of A and BK rows of B per stage).
+  // This lane's source byte offsets for its wave's chunks of stage 0, from the
+  // uniform bases A + m0 K and B + n0 (advanced by BK columns of A and BK rows of
+  // B per stage), less each instruction's immediate offset.  The launcher keeps
+  // BM K and 32 N below 2^30 floats, so they fit 32 bits; row >= 8 ii (A) and
+  // (e / BN) N + e % BN >= e >= 256 ii (B, N >= BN) keep them non-negative.
   const int jr = lane / 8, jp = lane % 8;
-  const float* srcA[NA];
-  const float* srcB[NB];
+  uint32_t offA[NA], offB[NB];
 #pragma unroll
   for (int ii = 0; ii < NA; ++ii) {
     const int ch = wave * NA + ii;
     const int row = 8 * ch + jr;
     const int slot = jp ^ jr ^ (ch & 1);          // f(row) = jr ^ (ch & 1)
-    srcA[ii] = A + static_cast<int64_t>(m0 + row) * K + 4 * slot;
+    offA[ii] = (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + 4u * slot) * 4u -
+               1024u * (ii % 4);
   }
 #pragma unroll
   for (int ii = 0; ii < NB; ++ii) {
     const int e = (wave * NB + ii) * 256 + 4 * lane;
-    srcB[ii] = B + static_cast<int64_t>(e / BN) * N + n0 + e % BN;
+    offB[ii] = (static_cast<uint32_t>(e / BN) * static_cast<uint32_t>(N) + e % BN) * 4u -
+               1024u * (ii % 4);
   }
-  const int64_t stepB = static_cast<int64_t>(BK) * N;
+  const char* a_base = reinterpret_cast<const char*>(A + static_cast<int64_t>(m0) * K);
+  const char* b_base = reinterpret_cast<const char*>(B + n0);
+  const int64_t stepB_bytes = static_cast<int64_t>(BK) * N * 4;
+  const uint32_t wave_u = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(wave));
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) char*)(smem)));
 
   f32x16 acc[MT][NT];
 #pragma unroll
@@ -553,9 +584,11 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st) {
       const int kk = (st < ksteps ? st : ksteps - 1) * BK;
-#pragma unroll
-      for (int i = 0; i < L; ++i)
-        mfma_dma_issue(i, NA, NB, kAFloats, srcA, srcB, stepB, smem + st * kStageFloats, kk, wave);
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        (mfma_dma_issue<I, NA, NB>(kAFloats, offA, offB, a_base, b_base, stepB_bytes,
+                                   lds0 + st * kStageFloats * 4, kk, wave_u),
+         ...);
+      }(std::make_integer_sequence<int, L>{});
     }
   }
 
@@ -583,7 +616,7 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const float* stage = smem + (ks % STAGES) * kStageFloats;
-    float* next_stage = smem + ((ks + STAGES - 1) % STAGES) * kStageFloats;
+    const uint32_t next_stage = lds0 + ((ks + STAGES - 1) % STAGES) * kStageFloats * 4;
     const int kf = ks + STAGES - 1;
     const int k_next = (kf < ksteps ? kf : ksteps - 1) * BK;
 
@@ -609,10 +642,13 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
         }
         // The fetch of stage ks + STAGES - 1, spread over the first half of the
         // sub-steps so that its issue hides under the MFMAs.
-#pragma unroll
-        for (int i = 0; i < L; ++i)
-          if ((i * (P / 2)) / L == p)
-            mfma_dma_issue(i, NA, NB, kAFloats, srcA, srcB, stepB, next_stage, k_next, wave);
+        [&]<int... I>(std::integer_sequence<int, I...>) {
+          (((I * (P / 2)) / L == p
+                ? mfma_dma_issue<I, NA, NB>(kAFloats, offA, offB, a_base, b_base, stepB_bytes,
+                                            next_stage, k_next, wave_u)
+                : void()),
+           ...);
+        }(std::make_integer_sequence<int, L>{});
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
