@@ -237,15 +237,16 @@ int launch_online(const float* x, float* y, int64_t rows, int64_t cols, hipStrea
     // 32768 rows is one round of resident workgroups with 64 bytes per lane in
     // flight (measured 6.2 us vs 8.2 us for one float4 per lane at 128 columns).
     // Longer rows: two float4s per lane over more lanes.  At 32768 x 1024, 128
-    // lanes x 2 took 42.9 us (64 x 4: 43.4, 32 x 8: 44.5, 256 x 1: 45.1; a plain
-    // copy of the same bytes 42.7); at 32768 x 4096, 512-lane workgroups of one
+    // lanes x 2 took 42.9 us in 256-lane workgroups and 42.45 in 512-lane ones of
+    // four rows (64 x 4: 43.4, 32 x 8: 44.5, 256 x 1: 45.1; a one-wave float4 copy
+    // of the same bytes 41.1); at 32768 x 4096, 512-lane workgroups of one
     // row x 2 took 163.2 us (256 x 4: 172.9, 128 x 8: 178.0, 64 x 16: 181.4; the
     // copy 165.5); at 16384 x 8192, 1024-lane workgroups of one row x 2 took
     // 171.0 us (256 x 8: 176.5, 512 x 4: 187.2).
     if (cv <= 32) return launch_regs<8, 4>(x, y, rows, cols, s);
     if (cv <= 64) return launch_regs<16, 4>(x, y, rows, cols, s);
     if (cv <= 128) return launch_regs<64, 2>(x, y, rows, cols, s);
-    if (cv <= 256) return launch_regs<128, 2>(x, y, rows, cols, s);
+    if (cv <= 256) return launch_regs<128, 2, 512>(x, y, rows, cols, s);
     if (cv <= 512) return launch_regs<64, 8>(x, y, rows, cols, s);
     if (cv <= 1024) return launch_regs<512, 2, 512>(x, y, rows, cols, s);
     return launch_regs<1024, 2, 1024>(x, y, rows, cols, s);
