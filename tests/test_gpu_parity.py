@@ -319,6 +319,28 @@ def test_mfma_kernel_attrs_report_the_whole_tile_kernel(gpu):
 
 
 @pytest.mark.parametrize("tile", [(64, 64, 32, 4, 4), (32, 32, 32, 2, 2)])
+@pytest.mark.parametrize("mnk", [(128, 128, 32), (128, 128, 96), (192, 64, 160), (64, 128, 224),
+                                 (64, 64, 64)])
+def test_gemm_dma_ring_step_counts(gpu, orc, tile, mnk):
+    """Whole-tile launches of at most one round of tiles take the direct-to-LDS
+    kernel's deep ring (8 stages for the 64x64 tile, whose barrier comes every
+    other K step; 4 for 32x32, every step).  Odd and even K-step counts, down to
+    a single step, against the full reference (reference.hpp:199-211), and the
+    same bits on a second launch."""
+    m, n, k = mnk
+    a = orc.fill_random(m * k, 0x51A7 + k)
+    b = orc.fill_random(k * n, 0x7E57 + k)
+    t = gpu.GemmTile(*tile)
+    want = orc.gemm(a, b, np.zeros(m * n, np.float32), m, n, k)
+    poisoned = np.full(m * n, np.nan, np.float32)
+    got = run_gemm(gpu, a, b, poisoned, m, n, k, 1.0, 0.0, gpu.GemmVariant.kMfmaF32, t)
+    r = orc.compare(got, want, orc.tol_gemm(k), orc.abs_tol_gemm(k))
+    assert r.ok, str(r)
+    again = run_gemm(gpu, a, b, poisoned, m, n, k, 1.0, 0.0, gpu.GemmVariant.kMfmaF32, t)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
+@pytest.mark.parametrize("tile", [(64, 64, 32, 4, 4), (32, 32, 32, 2, 2)])
 @pytest.mark.parametrize("n", [32, 64, 192, 512, 1024, 100, 257])
 def test_gemm_wave_group_tiles(gpu, orc, tile, n):
     """The 64x64 and 32x32 tiles fold their wave groups' shares of K in a fixed
