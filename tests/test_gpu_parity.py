@@ -318,15 +318,21 @@ def test_mfma_kernel_attrs_report_the_whole_tile_kernel(gpu):
         assert at.max_blocks_per_sm_api >= 1 and at.local_bytes == 0, tile.astuple()
 
 
-@pytest.mark.parametrize("tile", [(64, 64, 32, 4, 4), (32, 32, 32, 2, 2)])
-@pytest.mark.parametrize("mnk", [(128, 128, 32), (128, 128, 96), (192, 64, 160), (64, 128, 224),
-                                 (64, 64, 64)])
+_DMA_STEP_CASES = (
+    [((64, 64, 32, 4, 4), mnk) for mnk in
+     [(128, 128, 32), (128, 128, 96), (192, 64, 160), (64, 128, 224), (64, 64, 64)]] +
+    [((32, 32, 32, 2, 2), mnk) for mnk in [(128, 128, 32), (128, 128, 96), (64, 96, 160)]] +
+    [((256, 256, 32, 16, 16), mnk) for mnk in [(256, 256, 32), (256, 512, 96), (512, 256, 160)]] +
+    [((128, 128, 32, 8, 8), mnk) for mnk in [(256, 256, 32), (128, 384, 96)]])
+
+
+@pytest.mark.parametrize("tile,mnk", _DMA_STEP_CASES)
 def test_gemm_dma_ring_step_counts(gpu, orc, tile, mnk):
-    """Whole-tile launches of at most one round of tiles take the direct-to-LDS
-    kernel's deep ring (8 stages for the 64x64 tile, whose barrier comes every
-    other K step; 4 for 32x32, every step).  Odd and even K-step counts, down to
-    a single step, against the full reference (reference.hpp:199-211), and the
-    same bits on a second launch."""
+    """Whole-tile launches take the direct-to-LDS kernel: a deep ring for at most
+    one round of tiles (8 stages for the 64x64 tile, whose barrier comes every
+    other K step; 4 for 32x32, every step) and the 2-stage ring of the 128x128 and
+    256x256 tiles.  Odd and even K-step counts, down to a single step, against the
+    full reference (reference.hpp:199-211), and the same bits on a second launch."""
     m, n, k = mnk
     a = orc.fill_random(m * k, 0x51A7 + k)
     b = orc.fill_random(k * n, 0x7E57 + k)
