@@ -247,9 +247,6 @@ struct MfmaCfg {
   int bm, bn, bk;
   MfmaFn even, vec, scalar;
   int even_threads;   // block size of `even` (the staged kernels use 256)
-  // Whole tiles when the launch is at most one round of workgroups (tiles <= CUs):
-  // a deeper stage ring for the same threads, or null to use `even`.
-  MfmaFn even_one_round = nullptr;
   // `even` is the direct-to-LDS kernel, whose per-lane source offsets are 32-bit
   // byte offsets within a tile's BM rows of A and 32 rows of B.
   bool even_dma = false;
@@ -264,31 +261,25 @@ struct MfmaCfg {
 #define MCKE_MFMA_CFG_DMA(BM, BN, ST, KS)                                             \
   {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST, KS>,                                \
    &gemm_mfma_kernel<BM, BN, 32, true, false>, &gemm_mfma_kernel<BM, BN, 32, false, false>, \
-   kDmaThreads<BM, BN, KS>, nullptr, true}
-#define MCKE_MFMA_CFG_DMA_ROUND(BM, BN, ST, KS, ST1)                                  \
-  {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST, KS>,                                \
-   &gemm_mfma_kernel<BM, BN, 32, true, false>, &gemm_mfma_kernel<BM, BN, 32, false, false>, \
-   kDmaThreads<BM, BN, KS>, &gemm_mfma_dma_kernel<BM, BN, ST1, KS>, true}
+   kDmaThreads<BM, BN, KS>, true}
 
-// 64 x 64 tiles serve small problems, whose single round of tiles would leave
-// one wave per SIMD; two wave groups per tile measured 102.8 vs 89.9 TFLOP/s at
-// 1024^3 and 122.9 vs 120.4 at 2048^3.  With one workgroup per CU, a K step
-// (~1000 MFMA cycles) is short next to a load's round trip, so such a launch
-// takes a ring of 8 stages (128 KiB of LDS) instead of 4: 100.1-100.4 vs
-// 91.3-92.8 TFLOP/s at 1024^3 on one box, the same bits.  At more than one
-// round the 4-stage ring stays: it fits two workgroups per CU (2048^3 with 64 x
-// 64 tiles: 124.0 vs 114.8 TFLOP/s).  For 128 x 128 they bought nothing
-// (124.9 vs 124.7 at 2048^3, 130.6 vs 134.3 at 4096^3).  32 x 32 tiles (one wave
+// 64 x 64 tiles serve small problems, whose single round of tiles leaves one
+// workgroup per CU.  Their direct-to-LDS kernel meets at its barrier in the
+// middle of a K step and keeps the fragment reads one sub-step ahead across it,
+// so one wave group of 4 waves and a 4-stage ring measured best (1024^3: 109-110
+// TFLOP/s vs 106-107 with two wave groups and 99-106 with the earlier 8-stage
+// two-group ring; 2048^3 with 64 x 64 tiles: 134-135 vs 131; 3072^3: 136.5 vs
+// 134; 3, 5, 6 and 8 stages all measured slower).  For 128 x 128 a 4-stage ring
+// bought nothing over 2 at 2048^3 (137-139 either way).  32 x 32 tiles (one wave
 // wide, four groups) give the smallest problems four times the workgroups of
 // 64 x 64: 40.0 vs 22.6 TFLOP/s at 512^3, 7.0 vs 4.5 at 256^3.
 const MfmaCfg kMfmaCfgs[] = {
     MCKE_MFMA_CFG_DMA(256, 256, 2, 1), MCKE_MFMA_CFG(256, 256, 16),
     MCKE_MFMA_CFG_DMA(128, 128, 2, 1), MCKE_MFMA_CFG(128, 128, 16),
-    MCKE_MFMA_CFG_DMA_ROUND(64, 64, 4, 2, 8), MCKE_MFMA_CFG_DMA(32, 32, 4, 4),
+    MCKE_MFMA_CFG_DMA(64, 64, 4, 1), MCKE_MFMA_CFG_DMA(32, 32, 4, 4),
 };
 #undef MCKE_MFMA_CFG
 #undef MCKE_MFMA_CFG_DMA
-#undef MCKE_MFMA_CFG_DMA_ROUND
 
 const MfmaCfg* find_mfma(const mcke_gemm_tile& t) {
   for (const MfmaCfg& c : kMfmaCfgs)
@@ -301,7 +292,6 @@ struct Spec {
   GemmFn fn = nullptr;
   MfmaFn mfma = nullptr;
   MfmaFn mfma_even = nullptr;     // unchecked 16-byte variant for whole tiles
-  MfmaFn mfma_even_one_round = nullptr;   // the same for at most one round of tiles
   int even_threads = 0;           // their block size
   bool even_dma = false;          // they take 32-bit per-lane source offsets
   dim3 block{1, 1, 1};
@@ -363,7 +353,6 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
                        "(64,64,32,4,4) and (32,32,32,2,2); no fallback is applied");
       s.mfma = vec4 ? cfg->vec : cfg->scalar;
       s.mfma_even = vec4 ? cfg->even : nullptr;
-      s.mfma_even_one_round = vec4 ? cfg->even_one_round : nullptr;
       s.even_threads = cfg->even_threads;
       s.even_dma = cfg->even_dma;
       s.tile_k = cfg->bk;
@@ -462,8 +451,6 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
                        (!sp.even_dma || (static_cast<int64_t>(sp.tile_m) * k < (int64_t{1} << 30) &&
                                          static_cast<int64_t>(32) * n < (int64_t{1} << 30)));
     MfmaFn fn = whole ? sp.mfma_even : sp.mfma;
-    if (whole && sp.mfma_even_one_round && tiles_m * tiles_n <= device_cu_count())
-      fn = sp.mfma_even_one_round;
     const dim3 block = whole ? dim3(static_cast<unsigned>(sp.even_threads), 1, 1) : sp.block;
     fn<<<static_cast<unsigned>(tiles_m * tiles_n), block, 0, s>>>(
         a, b, c, mi, ni, ki, alpha, beta, static_cast<int>(tiles_m), static_cast<int>(tiles_n));
@@ -541,8 +528,8 @@ int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile*
   // tile area: partial rounds and the padding of edge tiles both count against
   // it); the best score wins (ties: larger tile).
   // Rates measured on MI355X (gfx950, 256 CUs), fp32, whole-tile shapes: 256 x 256
-  // (one workgroup per CU) ~145, 128 x 128 (two per CU) ~137, 64 x 64 (two wave
-  // groups per tile) ~128, 32 x 32 (four groups) ~100 TFLOP/s.  The scores pick the measured winner at every shape timed:
+  // (one workgroup per CU) ~145, 128 x 128 (two per CU) ~137, 64 x 64 ~135, 32 x 32
+  // (four wave groups) ~100 TFLOP/s.  The scores pick the measured winner at every shape timed:
   // 8192^3 and 8192 x 8192 x {512..2048} -> 256; 4096^3 -> 256 (140 vs 131);
   // 6144^3 -> 128 (137 vs 107 for 256, 2.25 rounds); 2048^3 and 2048 x 2048 x
   // 8192 -> 128 (125 vs 120 for 64); 3072^3 -> 64 (125 vs 101); 1024^3 -> 64
@@ -551,7 +538,7 @@ int mcke_gemm_mfma_default_tile(int64_t m, int64_t n, int64_t k, mcke_gemm_tile*
   struct Cand { int t; double rate; mcke_gemm_tile tile; };
   static const Cand cands[] = {{256, 145.0, {256, 256, 32, 16, 16}},
                                {128, 137.0, {128, 128, 32, 8, 8}},
-                               {64, 128.0, {64, 64, 32, 4, 4}},
+                               {64, 135.0, {64, 64, 32, 4, 4}},
                                {32, 100.0, {32, 32, 32, 2, 2}}};
   const int64_t cus = device_cu_count();
   double best = -1.0;

@@ -494,11 +494,10 @@ __device__ __forceinline__ void mfma_dma_issue(int a_floats, const uint32_t (&of
 // grid, or 1 x 1 for a 32 x 32 tile): group g runs the MFMA sub-steps of k-quarters [g Q/KS, (g+1) Q/KS)
 // of every stage into accumulators of its own, all groups read the same LDS
 // stages, and at the end groups 1 .. KS-1 hand their accumulators to group 0
-// through LDS, which adds them in group order and writes C.  It puts KS waves on
-// each SIMD for the same tile, so one wave's LDS waits and barrier skew hide
-// under another's MFMAs -- the case of small problems, whose one round of tiles
-// leaves one wave per SIMD.  The sum order over K differs from KS = 1 (the
-// groups' partials are added last), and is fixed for a given KS.
+// through LDS, which adds them in group order and writes C.  The 32 x 32 tile,
+// one wave wide and high, uses it to give its workgroup four waves.  The sum
+// order over K differs from KS = 1 (the groups' partials are added last), and is
+// fixed for a given KS.
 template <int BM, int BN, int STAGES, int KS = 1>
 __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
@@ -577,15 +576,12 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   const int ksteps = K / BK;
-  // Steps per barrier: rings of five or more stages meet every other step (see
-  // the loop below), others every step.
-  constexpr int SPB = STAGES >= 5 ? 2 : 1;
-  // Prologue: stages 0 .. STAGES-SPB-1 in flight.  Past the last K step a stage
+  // Prologue: stages 0 .. STAGES-2 in flight.  Past the last K step a stage
   // re-fetches the last one into a buffer nobody reads, which keeps the number of
   // loads per stage -- and so the vmcnt arithmetic below -- uniform.
   if (ksteps > 0) {
 #pragma unroll
-    for (int st = 0; st < STAGES - SPB; ++st) {
+    for (int st = 0; st < STAGES - 1; ++st) {
       const int kk = (st < ksteps ? st : ksteps - 1) * BK;
       [&]<int... I>(std::integer_sequence<int, I...>) {
         (mfma_dma_issue<I, NA, NB>(kAFloats, offA, offB, a_base, b_base, stepB_bytes,
@@ -612,14 +608,10 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
     // the second half.  The fragment reads run one sub-step ahead of the MFMAs,
     // across the barrier and across steps, so the matrix pipe does not drain at
     // the barrier or wait on a fresh fragment read at the top of a step (1024^3,
-    // 64 x 64 tile, 8 stages: 103.6-104.3 vs 100.5 TFLOP/s; reading B two
-    // sub-steps ahead measured the same).
-    // With SPB = 2 the barrier comes in the middle of even steps only: it
-    // publishes stages ks + 1 and ks + 2 and retires ks - 1 and ks - 2, and every
-    // step fetches stage ks + STAGES - 2 into the buffer of ks - 2 (retired by the
-    // barrier of step ks or, for odd ks, of step ks - 1).
+    // 64 x 64 tile, the two-group 8-stage ring of the time: 103.6-104.3 vs 100.5
+    // TFLOP/s; reading B two sub-steps ahead measured the same).
     if (ksteps > 0) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - SPB - 1) * L) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - 2) * L) : "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     }
@@ -631,20 +623,18 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
     for (int ks = 0; ks < ksteps; ++ks) {
       const float* stage = smem + (ks % STAGES) * kStageFloats;
       const float* stage_n = smem + ((ks + 1) % STAGES) * kStageFloats;
-      const uint32_t next_stage = lds0 + ((ks + STAGES - SPB) % STAGES) * kStageFloats * 4;
-      const int kf = ks + STAGES - SPB;
+      const uint32_t next_stage = lds0 + ((ks + STAGES - 1) % STAGES) * kStageFloats * 4;
+      const int kf = ks + STAGES - 1;
       const int k_next = (kf < ksteps ? kf : ksteps - 1) * BK;
-      const bool meet = SPB == 1 || ks % SPB == 0;
 #pragma unroll
       for (int qq = 0; qq < QG; ++qq) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const int p = 4 * qq + s;
-          if (p == P / 2 && meet) {
-            // Stages ks + 1 .. ks + SPB have landed once at most the (STAGES - 1 -
-            // 2 SPB) younger stages' loads are outstanding.  A bare s_barrier, as
-            // below.
-            asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - 1 - 2 * SPB) * L) : "memory");
+          if (p == P / 2) {
+            // Stage ks + 1 has landed once at most the (STAGES - 3) younger stages'
+            // loads are outstanding.  A bare s_barrier, as below.
+            asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - 3) * L) : "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
           }

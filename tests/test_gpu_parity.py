@@ -306,11 +306,11 @@ def test_gemm_512_baseline_config(gpu, orc):
 
 def test_mfma_kernel_attrs_report_the_whole_tile_kernel(gpu):
     """gemm_kernel_attrs (kernels.hpp:293-302) describes the kernel that whole-tile
-    shapes run: the 64x64 tile's direct-to-LDS kernel runs two wave groups (512
-    lanes), the larger tiles one (256 lanes), the 32x32 tile four one-wave groups
+    shapes run: the 64x64, 128x128 and 256x256 tiles' direct-to-LDS kernels run
+    one wave group of four waves (256 lanes), the 32x32 tile four one-wave groups
     (256 lanes)."""
     T = gpu.GemmTile
-    for tile, threads in ((T(32, 32, 32, 2, 2), 256), (T(64, 64, 32, 4, 4), 512),
+    for tile, threads in ((T(32, 32, 32, 2, 2), 256), (T(64, 64, 32, 4, 4), 256),
                           (T(128, 128, 32, 8, 8), 256), (T(256, 256, 32, 16, 16), 256)):
         st, at = gpu.gemm_kernel_attrs(gpu.GemmVariant.kMfmaF32, tile)
         assert st.ok(), str(st)
@@ -328,11 +328,11 @@ _DMA_STEP_CASES = (
 
 @pytest.mark.parametrize("tile,mnk", _DMA_STEP_CASES)
 def test_gemm_dma_ring_step_counts(gpu, orc, tile, mnk):
-    """Whole-tile launches take the direct-to-LDS kernel: a deep ring for at most
-    one round of tiles (8 stages for the 64x64 tile, whose barrier comes every
-    other K step; 4 for 32x32, every step) and the 2-stage ring of the 128x128 and
-    256x256 tiles.  Odd and even K-step counts, down to a single step, against the
-    full reference (reference.hpp:199-211), and the same bits on a second launch."""
+    """Whole-tile launches take the direct-to-LDS kernel: the 4-stage ring of the
+    64x64 and 32x32 tiles, whose barrier sits in the middle of a K step, and the
+    2-stage ring of the 128x128 and 256x256 tiles, whose barrier opens each step.
+    Odd and even K-step counts, down to a single step, against the full reference
+    (reference.hpp:199-211), and the same bits on a second launch."""
     m, n, k = mnk
     a = orc.fill_random(m * k, 0x51A7 + k)
     b = orc.fill_random(k * n, 0x7E57 + k)
@@ -349,11 +349,12 @@ def test_gemm_dma_ring_step_counts(gpu, orc, tile, mnk):
 @pytest.mark.parametrize("tile", [(64, 64, 32, 4, 4), (32, 32, 32, 2, 2)])
 @pytest.mark.parametrize("n", [32, 64, 192, 512, 1024, 100, 257])
 def test_gemm_wave_group_tiles(gpu, orc, tile, n):
-    """The 64x64 and 32x32 tiles fold their wave groups' shares of K in a fixed
-    order (whole tiles on the direct-to-LDS kernel; n = 100 and 257 on the staged
-    kernel, whose 32x32 tile also runs four groups): the full reference
-    (reference.hpp:199-211) at the K-scaled tolerance, the same bits on a second
-    launch, and beta = 0 never reading a NaN-poisoned C."""
+    """The small tiles: 64x64 (one wave group, 4-stage mid-step ring) and 32x32,
+    which folds its four wave groups' shares of K in a fixed order (whole tiles on
+    the direct-to-LDS kernel; n = 100 and 257 on the staged kernel, whose 32x32
+    tile also runs four groups): the full reference (reference.hpp:199-211) at the
+    K-scaled tolerance, the same bits on a second launch, and beta = 0 never
+    reading a NaN-poisoned C."""
     a = orc.fill_random(n * n, 0x6E33A + n)
     b = orc.fill_random(n * n, 0x8B10C + n)
     t = gpu.GemmTile(*tile)
