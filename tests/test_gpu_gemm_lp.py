@@ -59,8 +59,11 @@ def _quarters(rng, shape):
     return (rng.integers(-8, 9, size=shape) / 4.0).astype(np.float32)
 
 
+# The last four are whole tiles for the direct-to-LDS kernel with 1, 3, 5 and 7
+# K steps of 32 (its 4-stage ring's prologue and tail).
 QSHAPES = [(1, 1, 1), (5, 7, 3), (129, 65, 257), (1, 64, 128), (64, 1, 128), (33, 63, 1),
-           (253, 253, 253), (256, 256, 256), (512, 512, 512)]
+           (253, 253, 253), (256, 256, 256), (512, 512, 512),
+           (256, 256, 32), (256, 256, 96), (256, 512, 160), (512, 256, 224)]
 
 
 @pytest.mark.parametrize("dt", DTS, ids=DT_ID.get)
