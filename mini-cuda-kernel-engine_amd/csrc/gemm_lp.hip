@@ -22,9 +22,10 @@ template <int BM, int BN> struct LpDmaStages { static constexpr int value = 4; }
 
 template <typename T, typename OutT, int BM, int BN>
 struct LpTile {
-  // Whole tiles with 16-byte aligned operands take the direct-to-LDS kernel (tiles
+  // Whole tiles with 16-byte aligned operands take a direct-to-LDS kernel (tiles
   // with BN >= 128), whose per-lane source offsets are 32-bit: BM rows of A and 32
-  // rows of B must span less than 4 GiB.
+  // rows of B must span less than 4 GiB.  K % 64 == 0 takes the 16x16x32 kernel,
+  // the other multiples of 32 the 32x32x16 one.
   static bool use_dma(bool vec, int m, int n, int k) {
     if constexpr (BN < 128) {
       return false;
@@ -34,6 +35,7 @@ struct LpTile {
              static_cast<int64_t>(32) * n * 2 < (int64_t{1} << 32);
     }
   }
+  static bool use_dma16(int k) { return k % 64 == 0; }
 
   static int launch(const void* a, const void* b, void* c, int m, int n, int k, float alpha,
                     float beta, bool vec, hipStream_t s) {
@@ -49,9 +51,15 @@ struct LpTile {
     const int tmi = static_cast<int>(tiles_m), tni = static_cast<int>(tiles_n);
     if constexpr (BN >= 128) {
       if (use_dma(vec, m, n, k)) {
-        gemm_lp_dma_kernel<T, OutT, BM, BN, LpDmaStages<BM, BN>::value>
-            <<<grid, block, 0, s>>>(A, B, C, m, n, k, alpha, beta, tmi, tni);
-        MCKE_LAUNCH_CHECK("gemm_lp_dma_kernel");
+        if (use_dma16(k)) {
+          gemm_lp_dma16_kernel<T, OutT, BM, BN>
+              <<<grid, block, 0, s>>>(A, B, C, m, n, k, alpha, beta, tmi, tni);
+          MCKE_LAUNCH_CHECK("gemm_lp_dma16_kernel");
+        } else {
+          gemm_lp_dma_kernel<T, OutT, BM, BN, LpDmaStages<BM, BN>::value>
+              <<<grid, block, 0, s>>>(A, B, C, m, n, k, alpha, beta, tmi, tni);
+          MCKE_LAUNCH_CHECK("gemm_lp_dma_kernel");
+        }
         return ok();
       }
     }
@@ -72,7 +80,7 @@ struct LpTile {
     using Fn = void (*)(const uint16_t*, const uint16_t*, OutT*, int, int, int, float, float, int,
                         int);
     Fn fn;
-    if constexpr (BN >= 128) fn = &gemm_lp_dma_kernel<T, OutT, BM, BN, LpDmaStages<BM, BN>::value>;
+    if constexpr (BN >= 128) fn = &gemm_lp_dma16_kernel<T, OutT, BM, BN>;
     else fn = &gemm_lp_kernel<T, OutT, BM, BN, true, true>;
     return reinterpret_cast<LpKernel>(fn);
   }

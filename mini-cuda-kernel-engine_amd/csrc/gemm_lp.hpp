@@ -803,4 +803,464 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma_kernel(
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Whole-tile kernel on v_mfma_f32_16x16x32_{bf16,f16} (K % 64 == 0).
+//
+// Why this MFMA: with random operands the 16-bit matrix pipe is power-limited,
+// and per unit of work the 16x16x32 form draws less than the 32x32x16 one.  Long
+// chains of either at the same issue rate, on MI355X, settle at 1.82 GHz
+// (32x32x16) against 2.02 GHz (16x16x32); in the GEMM the engine clock is the
+// limit at 4096^3 and above.
+//
+// One v_mfma_f32_16x16x32 takes, per lane l, eight 16-bit A values of row l%16
+// and eight B values of column l%16; lane group g = l/16 covers k = 8 g .. 8 g + 7
+// of the 32 (A and B must agree on which k each group takes; the sum over k
+// does not care).  The result: lane l, register r = C row 4 g + r, column l%16.
+// A wave's WM x WN sub-tile is MT x NT blocks of 16 x 16 (MT = WM/16).
+//
+// Fragments per K step (32 deep): A block i is one ds_read_b128 (lane l reads
+// row 16 i + l%16, one 16-byte chunk); B block j is two ds_read_b64_tr_b16
+// (t = 0, 1): lane r = 4 jq + qa of group g points at B row k = 8 g + 4 t + jq,
+// columns 16 j + 4 qa .. + 3, and receives column 16 j + r at rows 8 g + 4 t .. + 3.
+//
+// LDS (BM = BN = 256: 160 KiB, all of it):
+//   A: three buffers, each 64 k deep (two K steps): BM rows of 128 bytes, chunk
+//      c of row r at position c ^ (r % 8).  Step ks reads chunks 4 (ks % 2) + g.
+//      Measured on MI355X, this read of 16 rows x 4 chunks has no bank conflicts
+//      over 128-byte rows, while over 64-byte rows (A 32 deep) every XOR
+//      swizzle tried conflicts 2-way; and 128-byte rows make the DMA fetch whole
+//      cache lines (8 lanes per row, one line each).
+//   B: four buffers, one K step (32 rows of BN * 2 bytes) each; 16-byte chunk c
+//      of row k sits at c ^ (4 (k % 4) + 2 ((k / 8) % 2)).  One half-wave of a
+//      transposed read touches two chunks of rows k0 .. k0 + 3 and
+//      k0 + 8 .. k0 + 11: the last term separates the two row quads.
+//
+// Pipeline, per K step ks (fragments double-buffered in registers):
+//   barrier: publishes B step ks + 1 (and, for even ks + 1, its A buffer); every
+//            wave has by then waited for all its reads of step ks - 1's buffers;
+//   MFMAs of step ks (block-row order) from one register set, interleaved with
+//            the 24 fragment reads of step ks + 1 into the other set, spread over
+//            the whole step, and the DMA of B step ks + 3 and of half an A buffer
+//            (A pair (ks + 4) / 2), which refill buffers of step ks - 1 and
+//            earlier.  Block row i waits only for A block i of its own set.
+// Every step issues the same DMA (half an A buffer, one B step), so one vmcnt
+// count covers both rings.
+// ---------------------------------------------------------------------------
+template <typename T> struct LpMfma16;
+template <> struct LpMfma16<__bf16> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct LpMfma16<_Float16> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <int BM, int BN>
+struct Lp16Shape {
+  static constexpr int BK = 32;                          // K per step
+  static constexpr int kAStages = 3, kBStages = 4;
+  static constexpr int kARow = 128;                      // A buffer row: 64 k
+  static constexpr int kABuf = BM * kARow;               // one A buffer (two steps)
+  static constexpr int kBRow = BN * 2;                   // 256 or 512 bytes
+  static constexpr int kBBytes = BK * kBRow;             // one B step
+  static constexpr int kBBase = kAStages * kABuf;        // B ring after the A ring
+  static constexpr int kLdsBytes = kBBase + kBStages * kBBytes;
+  static constexpr int NA = kABuf / 1024 / 4 / 2;        // A DMA instructions per wave per step
+  static constexpr int NB = kBBytes / 1024 / 4;          // B DMA instructions per wave per step
+  static constexpr int L = NA + NB;
+  static constexpr int kBChunksPerRow = BN / 8;
+  static constexpr int kBRowsPerChunk = 1024 / kBRow;
+  static constexpr int MT = BM / 32, NT = BN / 32;       // 16 x 16 blocks per wave
+  static constexpr int kMfmas = MT * NT;                 // per step
+  static_assert(BN == 128 || BN == 256, "B rows of 16 or 32 chunks");
+  static_assert(kABuf % 8192 == 0 && kBBytes % 4096 == 0, "buffers must split over 4 waves");
+  static_assert((kBStages - 2) * L <= 63, "vmcnt counts at most 63 loads");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS holds 160 KiB");
+  static_assert(NA <= 4 && NB <= 4, "DMA immediate offsets stay below 4 KiB");
+
+  static __host__ __device__ constexpr int bswz(int k) { return 4 * (k % 4) + 2 * ((k / 8) % 2); }
+
+  // A half h (0, 1) of the A buffer at LDS `abuf`, fetched from pair `pair` (64 k).
+  // Wave w's share of a buffer is 2 NA KiB at 2 NA w KiB; half h is NA KiB of it.
+  template <int II>
+  static __device__ __forceinline__ void dma_a(const char* a_base, const uint32_t (&a_src)[2 * NA],
+                                               int pair, int h, uint32_t abuf, uint32_t wave) {
+    const char* src = a_base + static_cast<int64_t>(pair) * kARow;
+    const uint32_t m0 = abuf + (wave * (2 * NA) + h * NA) * 1024;
+    lds_dma16<II * 1024>(h ? a_src[NA + II] : a_src[II], src, m0);
+  }
+  template <int II>
+  static __device__ __forceinline__ void dma_b(const char* b_base, int64_t b_step,
+                                               const uint32_t (&b_src)[NB], int kstep,
+                                               uint32_t bbuf, uint32_t wave) {
+    lds_dma16<II * 1024>(b_src[II], b_base + kstep * b_step, bbuf + wave * (NB * 1024));
+  }
+
+  // B block j (RR / 2), transposed read t = RR % 2, of the B buffer at `bst`.
+  template <int RR>
+  static __device__ __forceinline__ void read_b(uint32_t bst, const uint32_t (&b_off)[NT],
+                                                u32x2 (&bv)[NT][2]) {
+    constexpr int j = RR / 2, t = RR % 2;
+    bv[j][t] = lds_read_tr16<4 * t * kBRow>(bst + b_off[j]);
+  }
+  // A block I of a step whose chunk-adjusted base is `ast`.
+  template <int I>
+  static __device__ __forceinline__ void read_a(uint32_t ast, u32x4 (&av)[MT]) {
+    av[I] = lds_read128<I * 16 * kARow>(ast);
+  }
+  // Reads of the next step: B blocks first (2 NT transposed reads), then A
+  // blocks 0 .. MT-1, read rr after MFMA rr * kMfmas / kReads.
+  static constexpr int kReads = 2 * NT + MT;
+  static constexpr int read_slot(int rr) { return rr * kMfmas / kReads; }
+  // Block row i waits for A block i of its set: at most the A reads issued after
+  // it (MT - 1 - i, in the previous step) and the reads of the next step issued so
+  // far may be pending.  lgkmcnt counts to 15; a smaller count only waits for
+  // older reads as well.
+  static constexpr int wait_before_row(int i) {
+    int n = MT - 1 - i;
+    for (int rr = 0; rr < kReads; ++rr) n += read_slot(rr) < i * NT ? 1 : 0;
+    return n < 15 ? n : 15;
+  }
+};
+
+// Waits until at most N LDS reads are outstanding, then re-defines the listed
+// fragment registers so that no MFMA using them is scheduled above the wait.
+template <int N>
+__device__ __forceinline__ void lds_wait_n() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
+}
+template <int FIRST, int LAST, int MT>
+__device__ __forceinline__ void touch_a(u32x4 (&av)[MT]) {
+#pragma unroll
+  for (int i = FIRST; i < LAST; ++i) asm volatile("" : "+v"(av[i]));
+}
+template <int FIRST, int LAST, int NT>
+__device__ __forceinline__ void touch_b(u32x2 (&bv)[NT][2]) {
+#pragma unroll
+  for (int j = FIRST; j < LAST; ++j) {
+    asm volatile("" : "+v"(bv[j][0]));
+    asm volatile("" : "+v"(bv[j][1]));
+  }
+}
+
+// Per-step addresses of gemm_lp_dma16_kernel (LDS byte addresses and DMA sources).
+struct Lp16Step {
+  uint32_t bst_next;   // B buffer of the next step
+  uint32_t ast_next;   // A fragment base of the next step (its buffer and chunk half)
+  uint32_t abuf_dma;   // A buffer that this step's DMA fills
+  uint32_t bbuf_dma;   // B buffer that this step's DMA fills
+  int a_pair;          // A pair (64 k) fetched into abuf_dma
+  int a_half;          // which half of it
+  int b_kstep;         // B step fetched into bbuf_dma
+};
+
+// MFMA IDX of a step (block i = IDX / NT, j = IDX % NT) from register set P, then
+// the reads of the next step (into set 1 - P) and the DMA instructions that fall
+// in its slot.
+template <typename T, bool TRANS, int BM, int BN, int P, int IDX>
+__device__ __forceinline__ void lp16_slot(f32x4 (&acc)[BM / 32][BN / 32],
+                                          u32x4 (&av)[2][BM / 32], u32x2 (&bv)[2][BN / 32][2],
+                                          const Lp16Step& sp, const uint32_t (&b_off)[BN / 32],
+                                          const char* a_base, const char* b_base, int64_t b_step,
+                                          const uint32_t (&a_src)[2 * Lp16Shape<BM, BN>::NA],
+                                          const uint32_t (&b_src)[Lp16Shape<BM, BN>::NB],
+                                          uint32_t wave) {
+  using S = Lp16Shape<BM, BN>;
+  constexpr int NT = S::NT;
+  constexpr int i = IDX / NT, j = IDX % NT;
+  if constexpr (j == 0) {
+    lds_wait_n<S::wait_before_row(i)>();
+    touch_a<i, i + 1>(av[P]);
+    if constexpr (i == 0) touch_b<0, NT>(bv[P]);
+  }
+  const u32x4 b = u32x4{bv[P][j][0][0], bv[P][j][0][1], bv[P][j][1][0], bv[P][j][1][1]};
+  // TRANS: operands swapped, the MFMA computes the transposed block (n rows, m columns).
+  if constexpr (TRANS) acc[i][j] = LpMfma16<T>::run(b, av[P][i], acc[i][j]);
+  else acc[i][j] = LpMfma16<T>::run(av[P][i], b, acc[i][j]);
+  __builtin_amdgcn_sched_barrier(0);
+  [&]<int... RR>(std::integer_sequence<int, RR...>) {
+    ((S::read_slot(RR) == IDX
+          ? (RR < 2 * NT ? S::template read_b<(RR < 2 * NT ? RR : 0)>(sp.bst_next, b_off, bv[1 - P])
+                         : S::template read_a<(RR < 2 * NT ? 0 : RR - 2 * NT)>(sp.ast_next,
+                                                                              av[1 - P]))
+          : void()),
+     ...);
+  }(std::make_integer_sequence<int, S::kReads>{});
+  [&]<int... II>(std::integer_sequence<int, II...>) {
+    ((II * S::kMfmas / S::L == IDX
+          ? (II < S::NA ? S::template dma_a<(II < S::NA ? II : 0)>(a_base, a_src, sp.a_pair,
+                                                                   sp.a_half, sp.abuf_dma, wave)
+                        : S::template dma_b<(II < S::NA ? 0 : II - S::NA)>(
+                              b_base, b_step, b_src, sp.b_kstep, sp.bbuf_dma, wave))
+          : void()),
+     ...);
+  }(std::make_integer_sequence<int, S::L>{});
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One accumulator, copied out of the accumulation registers where it is used.
+// The TRANS epilogue reads every accumulator through this: the copies the
+// compiler would make are shared by its two branches and get hoisted above them,
+// all 256 at once.
+__device__ __forceinline__ float acc_get(float a) {
+  float v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
+}
+
+template <typename T, typename OutT, int BM, int BN>
+__global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma16_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, OutT* __restrict__ C,
+    int M, int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
+  using S = Lp16Shape<BM, BN>;
+  constexpr int BK = S::BK;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MT = S::MT, NT = S::NT, NA = S::NA;
+  constexpr int L = S::L;
+  constexpr bool TRANS = sizeof(OutT) == 2;
+
+  __shared__ __attribute__((aligned(1024))) char smem[S::kLdsBytes];
+
+  int tm, tn;
+  mfma_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int wm = wave / 2, wn = wave % 2;
+  const int g = lane / 16, r16 = lane % 16;
+
+  // DMA sources: a wave-uniform base per step plus a per-lane byte offset, less
+  // the immediate offset of the instruction (its index within the step, times
+  // 1024), which the DMA adds to both addresses.
+  //   A: instruction q (0 .. 2 NA - 1) of wave w fills rows 8 (2 NA w + q) ..
+  //   + 7 of an A buffer; lane l the chunk at position l % 8 of row l / 8 there,
+  //   which holds chunk (l % 8) ^ (row % 8).  row >= 8 q and K >= 64 keep the
+  //   difference non-negative.
+  //   B: as gemm_lp_dma_kernel with this kernel's B swizzle; row >=
+  //   kBRowsPerChunk ii with N >= BN keeps it non-negative.
+  const char* a_base = reinterpret_cast<const char*>(A + static_cast<int64_t>(m0) * K);
+  const char* b_base = reinterpret_cast<const char*>(B + n0);
+  const int64_t b_step = static_cast<int64_t>(BK) * N * 2;        // bytes per step
+  uint32_t a_src[2 * NA], b_src[S::NB];
+#pragma unroll
+  for (int q = 0; q < 2 * NA; ++q) {
+    const int row = 8 * (wave * 2 * NA + q) + lane / 8;
+    const int cg = (lane % 8) ^ (row % 8);
+    a_src[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) * 2u + 16u * cg -
+               1024u * (q % NA);
+  }
+#pragma unroll
+  for (int ii = 0; ii < S::NB; ++ii) {
+    const int row = S::kBRowsPerChunk * (wave * S::NB + ii) + lane / S::kBChunksPerRow;
+    const int cg = (lane % S::kBChunksPerRow) ^ S::bswz(row);
+    b_src[ii] = static_cast<uint32_t>(row) * static_cast<uint32_t>(N) * 2u + 16u * cg -
+                1024u * ii;
+  }
+  const uint32_t wave_u = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(wave));
+
+  // Fragment addressing (bytes within a buffer).
+  //   A block i of a step with chunk half s: row wm*WM + 16 i + r16, chunk
+  //   4 s + g at position (4 s + g) ^ (r16 % 8) (the row base is a multiple of
+  //   16); block i adds 16 rows as an immediate.
+  uint32_t a_off[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+    a_off[s] = (wm * WM + r16) * S::kARow + 16 * ((4 * s + g) ^ (r16 % 8));
+  //   B block j, read t: lane r16 = 4 jq + qa reads row k = 8 g + 4 t + jq at
+  //   columns wn*WN + 16 j + 4 qa .. + 3 (read t adds 4 rows as an immediate).
+  const int jq = r16 / 4, qa = r16 % 4;
+  uint32_t b_off[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int col = wn * WN + 16 * j + 4 * qa;
+    const int k = 8 * g + jq;
+    b_off[j] = k * S::kBRow + 16 * ((col / 8) ^ S::bswz(k)) + (col % 8) * 2;
+  }
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t ldsb = lds0 + S::kBBase;
+  const int ksteps = K / BK;                    // even
+  const int last_pair = ksteps / 2 - 1;
+  u32x4 av[2][MT];
+  u32x2 bv[2][NT][2];
+
+  // The DMA that step ks (or, for ks < 0, the prologue in its place) issues: half
+  // ks % 2 of A pair (ks + 4) / 2 into that pair's buffer, and B step ks + 3.  Past
+  // the end the sources repeat the last pair / step into buffers nobody reads,
+  // which keeps the number of loads per step -- and so the vmcnt arithmetic --
+  // uniform.
+  auto dma_plan = [&](int ks, Lp16Step& sp) {
+    const int pair = (ks + 4) / 2;                  // ks >= -4
+    sp.a_pair = pair < last_pair ? pair : last_pair;
+    sp.a_half = ks & 1;
+    sp.abuf_dma = lds0 + (pair % S::kAStages) * S::kABuf;
+    const int kb = ks + 3;
+    sp.b_kstep = kb < ksteps ? kb : ksteps - 1;
+    sp.bbuf_dma = ldsb + (kb % S::kBStages) * S::kBBytes;
+  };
+
+  if (ksteps > 0) {
+    // Prologue: the DMA of steps -4 .. -1 (A pairs 0 and 1, B steps 0 .. 2; step -4
+    // has no B), in the order the loop keeps.
+#pragma unroll
+    for (int ks = -4; ks < 0; ++ks) {
+      Lp16Step sp;
+      dma_plan(ks, sp);
+      [&]<int... II>(std::integer_sequence<int, II...>) {
+        (S::template dma_a<II>(a_base, a_src, sp.a_pair, sp.a_half, sp.abuf_dma, wave_u), ...);
+      }(std::make_integer_sequence<int, NA>{});
+      if (ks >= -3) {
+        [&]<int... II>(std::integer_sequence<int, II...>) {
+          (S::template dma_b<II>(b_base, b_step, b_src, sp.b_kstep, sp.bbuf_dma, wave_u), ...);
+        }(std::make_integer_sequence<int, S::NB>{});
+      }
+    }
+    // A pair 0 and B step 0 have landed once the two younger steps' loads at most
+    // are outstanding.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"((S::kBStages - 2) * L) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // Step 0's fragments into set 0, in the order the loop reads them.
+    [&]<int... RR>(std::integer_sequence<int, RR...>) {
+      (S::template read_b<RR>(ldsb, b_off, bv[0]), ...);
+    }(std::make_integer_sequence<int, 2 * NT>{});
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      (S::template read_a<I>(lds0 + a_off[0], av[0]), ...);
+    }(std::make_integer_sequence<int, MT>{});
+  }
+
+  // Step ks from register set P.
+  auto step = [&]<int P>(int ks) {
+    Lp16Step sp;
+    dma_plan(ks, sp);
+    const int kn = ks + 1;
+    sp.bst_next = ldsb + (kn % S::kBStages) * S::kBBytes;
+    sp.ast_next = lds0 + ((kn / 2) % S::kAStages) * S::kABuf + (kn & 1 ? a_off[1] : a_off[0]);
+
+    // B step ks + 1 (and A's buffer for it) has landed once at most the younger
+    // step's loads are outstanding; the barrier publishes every wave's share and
+    // retires the buffers refilled in this step (each wave waited for its reads of
+    // them in the step before).  A bare s_barrier: __syncthreads() would drain
+    // every outstanding load (vmcnt(0)).
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"((S::kBStages - 3) * L) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      (lp16_slot<T, TRANS, BM, BN, P, I>(acc, av, bv, sp, b_off, a_base, b_base, b_step, a_src,
+                                         b_src, wave_u),
+       ...);
+    }(std::make_integer_sequence<int, S::kMfmas>{});
+  };
+  // K % 64 == 0: whole pairs of steps, set 0 then set 1.
+  for (int ks = 0; ks < ksteps; ks += 2) {
+    step.template operator()<0>(ks);
+    step.template operator()<1>(ks + 1);
+  }
+  // The accumulators stay in the accumulation registers past the loop: left to
+  // itself the compiler copies all of them out at once where the loop and the
+  // K == 0 path meet, more than the other register file holds.
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) asm volatile("" : "+a"(acc[i][j]));
+  // acc_get is inline asm, which the hazard checks do not see into: the last
+  // MFMA's results are ready well before these 16 cycles are over.
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+  // No LDS DMA may still be landing, and no LDS read outstanding, when the
+  // workgroup retires.
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+
+  using O = LpOut<OutT>;
+  if constexpr (!TRANS) {
+    // Lane (g, r16) of block (i, j), register r: row wm*WM + 16 i + 4 g + r,
+    // column wn*WN + 16 j + r16.  A 16-lane group stores 64 contiguous bytes of a
+    // row; blocks j and j + 1 (j even) complete one 128-byte line.
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * WM + 16 * i + 4 * g + r;
+        OutT* crow = C + static_cast<int64_t>(row) * N + n0 + wn * WN + r16;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          float v = alpha * acc[i][j][r];
+          if (beta != 0.0f) v += beta * O::to_f32(crow[16 * j]);
+          crow[16 * j] = O::from_f32(v);
+        }
+      }
+    }
+    return;
+  }
+  // Transposed blocks: lane (g, r16), register r of block (i, j) holds C row
+  // wm*WM + 16 i + r16, column wn*WN + 16 j + 4 g + r -- one quad of four
+  // adjacent columns.
+  struct alignas(4 * sizeof(OutT)) Quad { OutT v[4]; };
+  if (beta == 0.0f) {
+    // Staged through the (now idle) stage buffers so that the global stores are
+    // whole rows, as in gemm_lp_dma_kernel.  Chunk q of tile row r sits at
+    // q ^ (r % kChunks): the 16 rows of a half-wave's quads land on 16 distinct
+    // chunk positions.
+    constexpr int kRowBytes = BN * 2;
+    constexpr int kChunks = kRowBytes / 16;
+    static_assert(BM * kRowBytes <= S::kLdsBytes, "the C tile must fit the buffers");
+    static_assert(kChunks <= 32 && (BM * kChunks) % kMfmaThreads == 0, "tile rows per pass");
+    __syncthreads();   // every wave has finished reading the stage buffers
+    // Block row by block row: left to itself the scheduler converts every
+    // accumulator ahead of the barrier and runs out of registers.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int rt = wm * WM + 16 * i + r16;            // tile row
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int col = wn * WN + 16 * j + 4 * g;
+        Quad o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o.v[e] = O::from_f32(alpha * acc_get(acc[i][j][e]));
+        *reinterpret_cast<Quad*>(smem + rt * kRowBytes + (((col / 8) ^ (rt % kChunks)) * 16) +
+                                 (col % 8) * 2) = o;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+    constexpr int kRowsPerPass = kMfmaThreads / kChunks;
+    const int q = threadIdx.x % kChunks;
+#pragma unroll 4
+    for (int r0 = 0; r0 < BM; r0 += kRowsPerPass) {
+      const int rt = r0 + threadIdx.x / kChunks;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(smem + rt * kRowBytes + ((q ^ (rt % kChunks)) * 16));
+      *reinterpret_cast<u32x4*>(C + static_cast<int64_t>(m0 + rt) * N + n0 + 8 * q) = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    OutT* crow = C + static_cast<int64_t>(m0 + wm * WM + 16 * i + r16) * N + n0 + wn * WN + 4 * g;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      Quad* dst = reinterpret_cast<Quad*>(crow + 16 * j);
+      const Quad old = *dst;
+      Quad o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o.v[e] = O::from_f32(alpha * acc_get(acc[i][j][e]) + beta * O::to_f32(old.v[e]));
+      *dst = o;
+    }
+  }
+}
+
 }  // namespace mcke_amd

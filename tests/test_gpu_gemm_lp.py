@@ -192,7 +192,12 @@ def test_kernel_attrs(gpu):
             st, at = gpu.gemm_lp_kernel_attrs(ab, cd, tile)
             assert st.ok(), str(st)
             assert at.local_bytes == 0, (tile, ab, cd)        # no spills on the whole-tile path
-            assert at.static_smem_bytes == 2 * (tile.bm + tile.bn) * 128
+            if tile.bn >= 128:
+                # Direct-to-LDS kernel (K % 64 == 0): three A buffers of 64 k
+                # (bm x 128 bytes) and four B steps of 32 k (32 x bn x 2 bytes).
+                assert at.static_smem_bytes == 3 * tile.bm * 128 + 4 * 32 * tile.bn * 2
+            else:
+                assert at.static_smem_bytes == 2 * (tile.bm + tile.bn) * 128
             assert at.threads_per_block == 256 and at.max_blocks_per_sm_api >= 1
 
 
