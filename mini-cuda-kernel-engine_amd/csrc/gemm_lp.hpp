@@ -1,5 +1,8 @@
-// gemm_lp.hpp -- 16-bit-input GEMM on the CDNA4 matrix cores
-// (v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x16_f16), fp32 accumulation.
+// gemm_lp.hpp -- 16-bit-input GEMM on the CDNA4 matrix cores, fp32 accumulation.
+// Three kernels: gemm_lp_kernel (any shape, register-staged, 32x32x16 MFMAs, the
+// layout described first below), gemm_lp_dma_kernel (whole tiles, direct-to-LDS,
+// 32x32x16, K % 64 == 32) and gemm_lp_dma16_kernel (whole tiles, direct-to-LDS,
+// 16x16x32, K % 64 == 0), each described where it is defined.
 //
 // C[M,N] = alpha * A[M,K] B[K,N] + beta * C, row-major; A and B in bf16 or fp16,
 // C in fp32 or in the input type (rounded to nearest even on the store).
