@@ -865,6 +865,46 @@ def gemm_lp_section(m, stream, iters=10, with_peak=True, vendor_sizes=(8192, 409
         out["peak_note"] = (f"blocks = 2 x CUs, 4 waves each, 4 chains of "
                             f"v_mfma_f32_32x32x16_{{bf16,f16}}, {iters_pk} iterations (~8192^3 "
                             "launch length)")
+        # Engine clock under random operands that change with every MFMA, for the two
+        # 16-bit MFMA forms at equal flops (mcke_launch_mfma_clock_lp): the reason the
+        # GEMM's whole-tile kernel uses 16x16x32.  Alternating launches of ~45 ms.
+        ticks = D(blocks * 16)
+        rng = np.random.default_rng(0x51A7)
+        probe = {}
+        for dt in (DT.kBF16, DT.kF16):
+            vals = rng.uniform(-1.0, 1.0, 256 * 8 * 8).astype(np.float32)
+            bits = to_bf16_bits(vals) if int(dt) == int(DT.kBF16) else \
+                vals.astype(np.float16).view(np.uint16)
+            dbits = D.from_array(np.ascontiguousarray(bits))
+            it_ck = max(1, int(0.045 * 2.0e15 / m.mfma_clock_lp_flops(blocks, 1)))
+            res = {}
+            for rep in range(3):
+                for shape, label in ((0, "32x32x16"), (1, "16x16x32")):
+                    e0, e1 = m.Event(), m.Event()
+                    e0.record(stream)
+                    m.launch_mfma_clock_lp(dt, shape, dbits, sink, ticks, blocks, it_ck,
+                                           stream).throw_if_error()
+                    e1.record(stream)
+                    stream.synchronize()
+                    ms = e0.elapsed_ms(e1)
+                    tk = ticks.download(blocks * 2, np.uint64).reshape(blocks, 2).astype(np.float64)
+                    if rep > 0:   # the first round warms the part
+                        res.setdefault(label, []).append(
+                            (m.mfma_clock_lp_flops(blocks, it_ck) / (ms * 1e-3) / 1e12,
+                             float(np.mean(tk[:, 0] / (tk[:, 1] * 10.0)))))
+            probe[names[int(dt)]] = {
+                lab: {"tflops": round(float(np.median([v[0] for v in vs])), 1),
+                      "clock_ghz": round(float(np.median([v[1] for v in vs])), 3)}
+                for lab, vs in res.items()}
+            log(f"16-bit MFMA clock probe {names[int(dt)]}: " + ", ".join(
+                f"{lab} {v['tflops']} TFLOP/s at {v['clock_ghz']} GHz"
+                for lab, v in probe[names[int(dt)]].items()))
+        out["mfma_clock_probe"] = probe
+        out["mfma_clock_probe_note"] = (
+            f"blocks = 2 x CUs, 4 waves each; 8 (32x32x16) or 16 (16x16x32) MFMAs per "
+            f"iteration over 8 operand registers of random 16-bit values, {it_ck} iterations "
+            "(~45 ms); clock = s_memtime cycles / s_memrealtime span, mean over workgroups; "
+            "median of 2 alternating rounds after one warm-up round")
         log(f"measured 16-bit MFMA peak: bf16 {out['measured_peak_bf16_tflops']} TFLOP/s, "
             f"f16 {out['measured_peak_f16_tflops']} TFLOP/s")
     # Vendor library on the same shapes (bf16 -> bf16, rocBLAS gemm_ex), for comparison

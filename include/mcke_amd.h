@@ -318,6 +318,17 @@ int mcke_launch_stream_copy_f32(const float* x, float* y, int64_t n, void* strea
 uint64_t mcke_mfma_peak_lp_flops(int64_t blocks, int64_t iters);
 int mcke_launch_mfma_peak_lp(int ab_dtype, const float* seed, float* out, int64_t blocks,
                              int64_t iters, void* stream);
+/* Engine-clock probe for the 16-bit MFMA forms (no reference counterpart): chains
+ * whose operands change with every instruction, as a GEMM's do, from eight
+ * operand registers per lane of random 16-bit values (operand_bits: 256 lanes x
+ * 8 x 16 bytes, 16-byte aligned).  shape 0 runs v_mfma_f32_32x32x16_{bf16,f16}
+ * (4 chains per wave), shape 1 v_mfma_f32_16x16x32_{bf16,f16} (8 chains): the
+ * same flops per iteration.  out receives blocks x 256 sums; ticks (2 x blocks)
+ * receives, per workgroup, its s_memtime span (engine clock cycles) and its
+ * s_memrealtime span (100 MHz ticks), so clock = cycles / (ticks x 10 ns). */
+uint64_t mcke_mfma_clock_lp_flops(int64_t blocks, int64_t iters);
+int mcke_launch_mfma_clock_lp(int ab_dtype, int shape, const void* operand_bits, float* out,
+                              uint64_t* ticks, int64_t blocks, int64_t iters, void* stream);
 
 /* ---- host data generators (bench / test inputs) ----------------------------
  * The same map as the reference's fill_random (tests/reference.hpp:101-109):

@@ -220,6 +220,8 @@ def lib() -> C.CDLL:
         "mcke_launch_stream_copy_f32": (C.c_int, [_VP, _VP, _I64, _VP]),
         "mcke_mfma_peak_lp_flops": (C.c_uint64, [_I64, _I64]),
         "mcke_launch_mfma_peak_lp": (C.c_int, [C.c_int, _VP, _VP, _I64, _I64, _VP]),
+        "mcke_mfma_clock_lp_flops": (C.c_uint64, [_I64, _I64]),
+        "mcke_launch_mfma_clock_lp": (C.c_int, [C.c_int, C.c_int, _VP, _VP, _VP, _I64, _I64, _VP]),
         "mcke_launch_stream_triad_f32": (C.c_int, [_VP, _VP, _VP, C.c_float, _I64, _VP]),
         "mcke_fill_random_f32": (None, [_VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
         "mcke_fill_normal_f32": (None, [_VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
@@ -573,6 +575,19 @@ def mfma_peak_lp_flops(blocks: int, iters: int) -> int:
 def launch_mfma_peak_lp(ab_dtype, seed, out, blocks: int, iters: int, stream=None) -> Status:
     return _st(lib().mcke_launch_mfma_peak_lp(int(ab_dtype), _ptr(seed), _ptr(out), blocks, iters,
                                               _sh(stream)))
+
+
+def mfma_clock_lp_flops(blocks: int, iters: int) -> int:
+    return int(lib().mcke_mfma_clock_lp_flops(blocks, iters))
+
+
+def launch_mfma_clock_lp(ab_dtype, shape: int, operand_bits, out, ticks, blocks: int, iters: int,
+                         stream=None) -> Status:
+    """Engine-clock probe for the 16-bit MFMA forms: shape 0 = 32x32x16, 1 = 16x16x32
+    (see include/mcke_amd.h)."""
+    return _st(lib().mcke_launch_mfma_clock_lp(int(ab_dtype), int(shape), _ptr(operand_bits),
+                                               _ptr(out), _ptr(ticks), blocks, iters,
+                                               _sh(stream)))
 
 
 def launch_stream_triad_f32(b, c, a, scalar: float, n: int, stream=None) -> Status:

@@ -85,6 +85,118 @@ __global__ __launch_bounds__(kPeakThreads) void mfma_peak_lp_kernel(const float*
   out[static_cast<int64_t>(blockIdx.x) * kPeakThreads + threadIdx.x] = s;
 }
 
+// Engine-clock probe for the 16-bit matrix pipe.  The peak kernel above feeds
+// every MFMA the same operands; a GEMM's change with every instruction, and with
+// random operands the pipe draws more power and the clock management lowers the
+// engine clock.  Here each lane holds eight operand registers of random 16-bit
+// values (`bits`, 8 x 16 bytes per lane of the workgroup) and every MFMA takes a
+// different pair.  SHAPE 0 runs 4 chains of v_mfma_f32_32x32x16, SHAPE 1 8 chains of
+// v_mfma_f32_16x16x32: the same flops per iteration (8 x 32768).  The chains are
+// inline asm so that the compiler keeps them independent (it merges chains whose
+// inputs it can prove equal); each chain's next MFMA is at least three
+// instructions later, and the s_nops cover the result latency before the sums.
+// Lane 0 of each workgroup records its s_memtime (engine clock) and
+// s_memrealtime (100 MHz) spans in ticks[2 b], ticks[2 b + 1].
+template <bool BF16, int SHAPE>
+__global__ __launch_bounds__(kPeakThreads) void mfma_clock_lp_kernel(
+    const u32x4* __restrict__ bits, float* __restrict__ out, uint64_t* __restrict__ ticks,
+    int64_t iters) {
+  const uint64_t c0 = __builtin_amdgcn_s_memtime();
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  const u32x4* b = bits + threadIdx.x * 8;
+  const u32x4 o0 = b[0], o1 = b[1], o2 = b[2], o3 = b[3], o4 = b[4], o5 = b[5], o6 = b[6],
+              o7 = b[7];
+  float s = 0.0f;
+  if constexpr (SHAPE == 0) {
+    f32x16 x0 = {}, x1 = {}, x2 = {}, x3 = {};
+    for (int64_t it = 0; it < iters; ++it) {
+      if constexpr (BF16)
+        asm volatile(
+            "v_mfma_f32_32x32x16_bf16 %0, %4, %5, %0\n\t"
+            "v_mfma_f32_32x32x16_bf16 %1, %6, %7, %1\n\t"
+            "v_mfma_f32_32x32x16_bf16 %2, %8, %9, %2\n\t"
+            "v_mfma_f32_32x32x16_bf16 %3, %10, %11, %3\n\t"
+            "v_mfma_f32_32x32x16_bf16 %0, %5, %6, %0\n\t"
+            "v_mfma_f32_32x32x16_bf16 %1, %7, %8, %1\n\t"
+            "v_mfma_f32_32x32x16_bf16 %2, %9, %10, %2\n\t"
+            "v_mfma_f32_32x32x16_bf16 %3, %11, %4, %3\n\t"
+            "s_nop 7"
+            : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
+            : "v"(o0), "v"(o1), "v"(o2), "v"(o3), "v"(o4), "v"(o5), "v"(o6), "v"(o7));
+      else
+        asm volatile(
+            "v_mfma_f32_32x32x16_f16 %0, %4, %5, %0\n\t"
+            "v_mfma_f32_32x32x16_f16 %1, %6, %7, %1\n\t"
+            "v_mfma_f32_32x32x16_f16 %2, %8, %9, %2\n\t"
+            "v_mfma_f32_32x32x16_f16 %3, %10, %11, %3\n\t"
+            "v_mfma_f32_32x32x16_f16 %0, %5, %6, %0\n\t"
+            "v_mfma_f32_32x32x16_f16 %1, %7, %8, %1\n\t"
+            "v_mfma_f32_32x32x16_f16 %2, %9, %10, %2\n\t"
+            "v_mfma_f32_32x32x16_f16 %3, %11, %4, %3\n\t"
+            "s_nop 7"
+            : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
+            : "v"(o0), "v"(o1), "v"(o2), "v"(o3), "v"(o4), "v"(o5), "v"(o6), "v"(o7));
+    }
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += x0[r] + x1[r] + x2[r] + x3[r];
+  } else {
+    f32x4 x0 = {}, x1 = {}, x2 = {}, x3 = {}, x4 = {}, x5 = {}, x6 = {}, x7 = {};
+    for (int64_t it = 0; it < iters; ++it) {
+      if constexpr (BF16)
+        asm volatile(
+            "v_mfma_f32_16x16x32_bf16 %0, %8, %9, %0\n\t"
+            "v_mfma_f32_16x16x32_bf16 %1, %10, %11, %1\n\t"
+            "v_mfma_f32_16x16x32_bf16 %2, %12, %13, %2\n\t"
+            "v_mfma_f32_16x16x32_bf16 %3, %14, %15, %3\n\t"
+            "v_mfma_f32_16x16x32_bf16 %4, %9, %10, %4\n\t"
+            "v_mfma_f32_16x16x32_bf16 %5, %11, %12, %5\n\t"
+            "v_mfma_f32_16x16x32_bf16 %6, %13, %14, %6\n\t"
+            "v_mfma_f32_16x16x32_bf16 %7, %15, %8, %7\n\t"
+            "v_mfma_f32_16x16x32_bf16 %0, %10, %13, %0\n\t"
+            "v_mfma_f32_16x16x32_bf16 %1, %12, %15, %1\n\t"
+            "v_mfma_f32_16x16x32_bf16 %2, %14, %9, %2\n\t"
+            "v_mfma_f32_16x16x32_bf16 %3, %8, %11, %3\n\t"
+            "v_mfma_f32_16x16x32_bf16 %4, %11, %14, %4\n\t"
+            "v_mfma_f32_16x16x32_bf16 %5, %13, %8, %5\n\t"
+            "v_mfma_f32_16x16x32_bf16 %6, %15, %10, %6\n\t"
+            "v_mfma_f32_16x16x32_bf16 %7, %9, %12, %7\n\t"
+            "s_nop 7"
+            : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3), "+v"(x4), "+v"(x5), "+v"(x6), "+v"(x7)
+            : "v"(o0), "v"(o1), "v"(o2), "v"(o3), "v"(o4), "v"(o5), "v"(o6), "v"(o7));
+      else
+        asm volatile(
+            "v_mfma_f32_16x16x32_f16 %0, %8, %9, %0\n\t"
+            "v_mfma_f32_16x16x32_f16 %1, %10, %11, %1\n\t"
+            "v_mfma_f32_16x16x32_f16 %2, %12, %13, %2\n\t"
+            "v_mfma_f32_16x16x32_f16 %3, %14, %15, %3\n\t"
+            "v_mfma_f32_16x16x32_f16 %4, %9, %10, %4\n\t"
+            "v_mfma_f32_16x16x32_f16 %5, %11, %12, %5\n\t"
+            "v_mfma_f32_16x16x32_f16 %6, %13, %14, %6\n\t"
+            "v_mfma_f32_16x16x32_f16 %7, %15, %8, %7\n\t"
+            "v_mfma_f32_16x16x32_f16 %0, %10, %13, %0\n\t"
+            "v_mfma_f32_16x16x32_f16 %1, %12, %15, %1\n\t"
+            "v_mfma_f32_16x16x32_f16 %2, %14, %9, %2\n\t"
+            "v_mfma_f32_16x16x32_f16 %3, %8, %11, %3\n\t"
+            "v_mfma_f32_16x16x32_f16 %4, %11, %14, %4\n\t"
+            "v_mfma_f32_16x16x32_f16 %5, %13, %8, %5\n\t"
+            "v_mfma_f32_16x16x32_f16 %6, %15, %10, %6\n\t"
+            "v_mfma_f32_16x16x32_f16 %7, %9, %12, %7\n\t"
+            "s_nop 7"
+            : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3), "+v"(x4), "+v"(x5), "+v"(x6), "+v"(x7)
+            : "v"(o0), "v"(o1), "v"(o2), "v"(o3), "v"(o4), "v"(o5), "v"(o6), "v"(o7));
+    }
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s += x0[r] + x1[r] + x2[r] + x3[r] + x4[r] + x5[r] + x6[r] + x7[r];
+  }
+  out[static_cast<int64_t>(blockIdx.x) * kPeakThreads + threadIdx.x] = s;
+  if (threadIdx.x == 0) {
+    ticks[2 * static_cast<int64_t>(blockIdx.x)] = __builtin_amdgcn_s_memtime() - c0;
+    ticks[2 * static_cast<int64_t>(blockIdx.x) + 1] = __builtin_amdgcn_s_memrealtime() - r0;
+  }
+}
+
 constexpr int kTriadThreads = 256;
 
 __global__ __launch_bounds__(kTriadThreads) void stream_triad_kernel(const float* __restrict__ b,
@@ -177,6 +289,34 @@ int mcke_launch_mfma_peak_lp(int ab_dtype, const float* seed, float* out, int64_
     mfma_peak_lp_kernel<_Float16><<<static_cast<unsigned>(blocks), kPeakThreads, 0, s>>>(seed, out,
                                                                                          iters);
   MCKE_LAUNCH_CHECK("mfma_peak_lp_kernel");
+  return ok();
+}
+
+uint64_t mcke_mfma_clock_lp_flops(int64_t blocks, int64_t iters) {
+  if (blocks <= 0 || iters <= 0) return 0;
+  return static_cast<uint64_t>(blocks) * (kPeakThreads / kWave) * static_cast<uint64_t>(iters) * 8 *
+         kFlopsPerMfmaLp;
+}
+
+int mcke_launch_mfma_clock_lp(int ab_dtype, int shape, const void* operand_bits, float* out,
+                              uint64_t* ticks, int64_t blocks, int64_t iters, void* stream) {
+  if (ab_dtype != MCKE_DTYPE_BF16 && ab_dtype != MCKE_DTYPE_F16)
+    return invalid("launch_mfma_clock_lp: ab_dtype must be MCKE_DTYPE_BF16 or MCKE_DTYPE_F16");
+  if (shape != 0 && shape != 1)
+    return invalid("launch_mfma_clock_lp: shape must be 0 (32x32x16) or 1 (16x16x32)");
+  if (!operand_bits || !out || !ticks) return invalid("launch_mfma_clock_lp: null pointer");
+  if (!aligned(operand_bits, 16)) return invalid("launch_mfma_clock_lp: operand_bits not 16-byte aligned");
+  if (blocks <= 0 || blocks > 0x7fffffff) return invalid("launch_mfma_clock_lp: blocks out of range");
+  if (iters <= 0) return invalid("launch_mfma_clock_lp: iters must be > 0");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const auto* bits = static_cast<const u32x4*>(operand_bits);
+  const dim3 g(static_cast<unsigned>(blocks)), t(kPeakThreads);
+  const bool bf16 = ab_dtype == MCKE_DTYPE_BF16;
+  if (bf16 && shape == 0) mfma_clock_lp_kernel<true, 0><<<g, t, 0, s>>>(bits, out, ticks, iters);
+  else if (bf16) mfma_clock_lp_kernel<true, 1><<<g, t, 0, s>>>(bits, out, ticks, iters);
+  else if (shape == 0) mfma_clock_lp_kernel<false, 0><<<g, t, 0, s>>>(bits, out, ticks, iters);
+  else mfma_clock_lp_kernel<false, 1><<<g, t, 0, s>>>(bits, out, ticks, iters);
+  MCKE_LAUNCH_CHECK("mfma_clock_lp_kernel");
   return ok();
 }
 

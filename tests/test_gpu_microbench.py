@@ -125,6 +125,82 @@ def test_mfma_peak_lp_closed_form(mcke, gpu, dt):
         m.StatusCode.kInvalidArgument
 
 
+# Operand-register pairs (A, B) of each chain's two MFMAs per iteration in the clock
+# probe (mfma_clock_lp_kernel): 4 chains of 32x32x16, or 8 chains of 16x16x32.
+_CLOCK_PAIRS = {
+    0: [[(0, 1), (1, 2)], [(2, 3), (3, 4)], [(4, 5), (5, 6)], [(6, 7), (7, 0)]],
+    1: [[(0, 1), (2, 5)], [(2, 3), (4, 7)], [(4, 5), (6, 1)], [(6, 7), (0, 3)],
+        [(1, 2), (3, 6)], [(3, 4), (5, 0)], [(5, 6), (7, 2)], [(7, 0), (1, 4)]],
+}
+
+
+def _mfma_clock_lp_expected(vals: np.ndarray, shape: int, blocks: int, iters: int) -> np.ndarray:
+    """out[block*256 + t] of the clock probe.  vals[t, k, e]: element e of operand
+    register k of thread t.  Whatever k each (lane group, element) slot stands for, A
+    and B share it.  32x32x16: C[i][j] = sum over h, e of A(lane i + 32h, e) B(lane
+    j + 32h, e), lane l register r holding C[8 (r/4) + 4 (l/32) + r%4][l%32].
+    16x16x32: C[i][j] = sum over g, e of A(lane i + 16g, e) B(lane j + 16g, e), lane l
+    register r holding C[4 (l/16) + r][l%16]."""
+    out = np.zeros(256, dtype=np.float64)
+    n, groups = (32, 2) if shape == 0 else (16, 4)
+    for w in range(4):
+        v = vals[64 * w:64 * w + 64].astype(np.float64)          # [lane, k, e]
+        for pairs in _CLOCK_PAIRS[shape]:
+            c = np.zeros((n, n))
+            for ka, kb in pairs:
+                for g in range(groups):
+                    a = v[n * g:n * g + n, ka, :]                  # [i, e]
+                    b = v[n * g:n * g + n, kb, :]                  # [j, e]
+                    c += a @ b.T
+            c *= iters
+            for l in range(64):
+                if shape == 0:
+                    out[64 * w + l] += sum(c[8 * (r // 4) + 4 * (l // 32) + r % 4, l % 32]
+                                           for r in range(16))
+                else:
+                    out[64 * w + l] += sum(c[4 * (l // 16) + r, l % 16] for r in range(4))
+    return np.tile(out, blocks).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", [2, 1], ids=["bf16", "f16"])
+@pytest.mark.parametrize("shape", [0, 1], ids=["32x32x16", "16x16x32"])
+def test_mfma_clock_lp_closed_form_and_clock(mcke, gpu, dt, shape):
+    """The clock probe computes what its operand rotation says (exact: small integers),
+    and reports a plausible clock."""
+    m = mcke
+    vals = ((np.arange(256 * 8 * 8) * 5 + 3) % 7 - 3).astype(np.float32).reshape(256, 8, 8)
+    if dt == 2:
+        bits = (vals.reshape(-1).view(np.uint32) >> 16).astype(np.uint16)   # exact values
+    else:
+        bits = vals.reshape(-1).astype(np.float16).view(np.uint16)
+    blocks, iters = 2, 50
+    d_bits = m.DeviceBuffer.from_array(bits)
+    out = m.DeviceBuffer(blocks * 256 * 4)
+    ticks = m.DeviceBuffer(blocks * 16)
+    m.launch_mfma_clock_lp(dt, shape, d_bits, out, ticks, blocks, iters).throw_if_error()
+    m.device_synchronize()
+    got = out.download(blocks * 256)
+    assert np.array_equal(got, _mfma_clock_lp_expected(vals, shape, blocks, iters))
+    tk = ticks.download(blocks * 2, np.uint64).reshape(blocks, 2).astype(np.float64)
+    assert (tk > 0).all()
+    ghz = tk[:, 0] / (tk[:, 1] * 10.0)
+    assert ((ghz > 0.3) & (ghz < 4.0)).all(), ghz
+    assert m.mfma_clock_lp_flops(blocks, iters) == blocks * 4 * iters * 8 * 32768
+
+
+def test_mfma_clock_lp_rejects(mcke, gpu):
+    m = mcke
+    b, o, t = m.DeviceBuffer(32768), m.DeviceBuffer(4096), m.DeviceBuffer(64)
+    IA = m.StatusCode.kInvalidArgument
+    assert m.launch_mfma_clock_lp(0, 0, b, o, t, 1, 1).code == IA       # fp32
+    assert m.launch_mfma_clock_lp(2, 2, b, o, t, 1, 1).code == IA       # no such shape
+    assert m.launch_mfma_clock_lp(2, 0, b.ptr + 8, o, t, 1, 1).code == IA
+    assert m.launch_mfma_clock_lp(2, 0, b, o, t, 0, 1).code == IA
+    assert m.launch_mfma_clock_lp(2, 0, b, o, t, 1, 0).code == IA
+    assert m.launch_mfma_clock_lp(2, 0, None, o, t, 1, 1).code == IA
+    assert m.mfma_clock_lp_flops(0, 1) == 0
+
+
 @pytest.mark.parametrize("n", [1, 3, 4, 7, 1000, 4097, 1 << 20])
 def test_stream_copy_exact(mcke, gpu, n):
     m = mcke
