@@ -367,9 +367,7 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
     default:
       return invalid("launch_gemm_f32: unknown GemmVariant " + std::to_string(variant));
   }
-  // Attribute queries report the instantiation that whole-tile shapes run (for a
-  // launch of at most one round of tiles the 64 x 64 tile runs a deeper stage
-  // ring of the same kernel: same lanes, more LDS).
+  // Attribute queries report the instantiation that whole-tile shapes run.
   s.kernel = s.fn ? reinterpret_cast<const void*>(s.fn)
                   : reinterpret_cast<const void*>(s.mfma_even ? s.mfma_even : s.mfma);
   return ok();
