@@ -332,7 +332,10 @@ def test_gemm_dma_ring_step_counts(gpu, orc, tile, mnk):
     64x64 and 32x32 tiles, whose barrier sits in the middle of a K step, and the
     2-stage ring of the 128x128 and 256x256 tiles, whose barrier opens each step.
     Odd and even K-step counts, down to a single step, against the full reference
-    (reference.hpp:199-211), and the same bits on a second launch."""
+    (reference.hpp:199-211), and the same bits on a second launch.  The whole-tile
+    epilogue stores 16 bytes per lane (8 for the 128x128 tile, whose lanes hold two
+    adjacent columns; the 64x64 and 32x32 tiles transpose 4x4 blocks across lane
+    quads first), so alpha / beta are checked on every tile too."""
     m, n, k = mnk
     a = orc.fill_random(m * k, 0x51A7 + k)
     b = orc.fill_random(k * n, 0x7E57 + k)
@@ -344,6 +347,11 @@ def test_gemm_dma_ring_step_counts(gpu, orc, tile, mnk):
     assert r.ok, str(r)
     again = run_gemm(gpu, a, b, poisoned, m, n, k, 1.0, 0.0, gpu.GemmVariant.kMfmaF32, t)
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    c0 = orc.fill_random(m * n, 0xC0FFEE + k)
+    got = run_gemm(gpu, a, b, c0, m, n, k, 0.5, 2.0, gpu.GemmVariant.kMfmaF32, t)
+    want = orc.gemm(a, b, c0, m, n, k, 0.5, 2.0)
+    r = orc.compare(got, want, orc.tol_gemm(k), orc.abs_tol_gemm(k) * 2.0)
+    assert r.ok, str(r)
 
 
 @pytest.mark.parametrize("tile", [(64, 64, 32, 4, 4), (32, 32, 32, 2, 2)])
