@@ -675,7 +675,89 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
   for (int qq = 0; qq < QG; ++qq) a_q[qq] = 4 * ((4 * h + kg * QG + qq) ^ f);
   const int b_off = kAFloats + (h * (BK / 2) + 4 * kg * QG) * BN + wn * WN + NT * c;
 
-  if constexpr (STAGES >= 3) {
+  if constexpr (STAGES >= 3 && KS > 1) {
+    // The ring with its barrier in the middle of a step (as below), for wave
+    // groups that split K: a group's share of a stage is only P = 4 QG sub-steps,
+    // too short for reads one sub-step ahead to hide LDS latency.  Instead all of
+    // stage ks + 1's fragments are read right after the barrier that publishes it,
+    // into the other of two register sets, while the second half of stage ks's
+    // MFMAs runs; the next step's MFMAs then never wait on a read (32 x 32 tile at
+    // 512^3: 5.27 vs 5.88 us, the same bits; for the 64 x 64 tile, one group of 16
+    // sub-steps, it measured slower than the reads one ahead: 20.0 vs 19.2 us at
+    // 1024^3).  Steps come in pairs so that the register sets alternate by name.
+    if (ksteps > 0) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - 2) * L) : "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+    static_assert(P % 2 == 0 && QG <= P / 2, "reads of the next stage fit the second half");
+    f32x4 af[2][QG][MT];
+    BV bf[2][P];
+#pragma unroll
+    for (int qq = 0; qq < QG; ++qq)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+        af[0][qq][i] = *reinterpret_cast<const f32x4*>(smem + a_row + i * 32 * BK + a_q[qq]);
+#pragma unroll
+    for (int p = 0; p < P; ++p) bf[0][p] = *reinterpret_cast<const BV*>(smem + b_off + p * BN);
+    auto step = [&]<int PP>(int ks) {
+      // Past the last step the reads below fetch a buffer whose values go unused.
+      const float* stage_n = smem + ((ks + 1) % STAGES) * kStageFloats;
+      const uint32_t next_stage = lds0 + ((ks + STAGES - 1) % STAGES) * kStageFloats * 4;
+      const int kf = ks + STAGES - 1;
+      const int k_next = (kf < ksteps ? kf : ksteps - 1) * BK;
+#pragma unroll
+      for (int qq = 0; qq < QG; ++qq) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int p = 4 * qq + s;
+          if (p == P / 2) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"i"((STAGES - 3) * L) : "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+          }
+          if (p >= P / 2) {
+            // Sub-step P/2 + x reads B rows 2x, 2x + 1 and, for x < QG, A quarter x.
+            const int x = p - P / 2;
+            bf[1 - PP][2 * x] = *reinterpret_cast<const BV*>(stage_n + b_off + (2 * x) * BN);
+            bf[1 - PP][2 * x + 1] =
+                *reinterpret_cast<const BV*>(stage_n + b_off + (2 * x + 1) * BN);
+            if (x < QG) {
+              const int xq = x < QG ? x : 0;   // (keeps the unrolled indices in range)
+#pragma unroll
+              for (int i = 0; i < MT; ++i)
+                af[1 - PP][xq][i] =
+                    *reinterpret_cast<const f32x4*>(stage_n + a_row + i * 32 * BK + a_q[xq]);
+            }
+          }
+          // The fetch of stage ks + STAGES - 1, spread over the second half.
+          [&]<int... I>(std::integer_sequence<int, I...>) {
+            ((P / 2 + (I * (P / 2)) / L == p
+                  ? mfma_dma_issue<I, NA, NB>(kAFloats, offA, offB, a_base, b_base, stepB_bytes,
+                                              next_stage, k_next, wave_u)
+                  : void()),
+             ...);
+          }(std::make_integer_sequence<int, L>{});
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+              float bj;
+              if constexpr (NT == 1) bj = bf[PP][p]; else bj = bf[PP][p][j];
+              acc[i][j] =
+                  __builtin_amdgcn_mfma_f32_32x32x2f32(af[PP][qq][i][s], bj, acc[i][j], 0, 0, 0);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+    for (int ks = 0; ks < ksteps; ks += 2) {
+      step.template operator()<0>(ks);
+      if (ks + 1 < ksteps) step.template operator()<1>(ks + 1);
+    }
+  } else if constexpr (STAGES >= 3) {
     // With three or more stages the barrier sits in the middle of a step: after
     // half of stage ks's sub-steps it publishes stage ks + 1 and retires the
     // buffer of stage ks - 1, whose fetch (stage ks + STAGES - 1) then issues over
