@@ -867,7 +867,14 @@ template <> struct LpMfma16<_Float16> {
 template <int BM, int BN>
 struct Lp16Shape {
   static constexpr int BK = 32;                          // K per step
-  static constexpr int kAStages = 3, kBStages = 4;
+  // Ring depth: step ks issues the DMA of B step ks + kDepth and of half of A pair
+  // (ks + kDepth + 1) / 2, so a step's operands have kDepth - 1 steps to land
+  // before the step before it reads them.  B keeps kDepth + 1 buffers, A
+  // kDepth / 2 + 2 pairs: a buffer is refilled only after the barrier that
+  // follows its last reads.
+  static constexpr int kDepth = 3;
+  static constexpr int kBStages = kDepth + 1;
+  static constexpr int kAStages = kDepth / 2 + 2;
   static constexpr int kARow = 128;                      // A buffer row: 64 k
   static constexpr int kABuf = BM * kARow;               // one A buffer (two steps)
   static constexpr int kBRow = BN * 2;                   // 256 or 512 bytes
@@ -884,6 +891,7 @@ struct Lp16Shape {
   static_assert(BN == 128 || BN == 256, "B rows of 16 or 32 chunks");
   static_assert(kABuf % 8192 == 0 && kBBytes % 4096 == 0, "buffers must split over 4 waves");
   static_assert((kBStages - 2) * L <= 63, "vmcnt counts at most 63 loads");
+  static_assert(2 * kAStages >= kDepth + 2 && kBStages >= kDepth, "buffers retire in time");
   static_assert(kLdsBytes <= 160 * 1024, "LDS holds 160 KiB");
   static_assert(NA <= 4 && NB <= 4, "DMA immediate offsets stay below 4 KiB");
 
@@ -1109,38 +1117,38 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma16_kernel(
   u32x2 bv[2][NT][2];
 
   // The DMA that step ks (or, for ks < 0, the prologue in its place) issues: half
-  // ks % 2 of A pair (ks + 4) / 2 into that pair's buffer, and B step ks + 3.  Past
-  // the end the sources repeat the last pair / step into buffers nobody reads,
-  // which keeps the number of loads per step -- and so the vmcnt arithmetic --
-  // uniform.
+  // ks % 2 of A pair (ks + D + 1) / 2 into that pair's buffer, and B step ks + D
+  // (D = kDepth).  Past the end the sources repeat the last pair / step into
+  // buffers nobody reads, which keeps the number of loads per step -- and so the
+  // vmcnt arithmetic -- uniform.
   auto dma_plan = [&](int ks, Lp16Step& sp) {
-    const int pair = (ks + 4) / 2;                  // ks >= -4
+    const int pair = (ks + S::kDepth + 1) / 2;      // ks >= -D - 1
     sp.a_pair = pair < last_pair ? pair : last_pair;
     sp.a_half = ks & 1;
     sp.abuf_dma = lds0 + (pair % S::kAStages) * S::kABuf;
-    const int kb = ks + 3;
+    const int kb = ks + S::kDepth;
     sp.b_kstep = kb < ksteps ? kb : ksteps - 1;
     sp.bbuf_dma = ldsb + (kb % S::kBStages) * S::kBBytes;
   };
 
   if (ksteps > 0) {
-    // Prologue: the DMA of steps -4 .. -1 (A pairs 0 and 1, B steps 0 .. 2; step -4
-    // has no B), in the order the loop keeps.
+    // Prologue: the DMA of steps -D - 1 .. -1 (A pairs 0 .. D / 2, B steps 0 ..
+    // D - 1; step -D - 1 has no B), in the order the loop keeps.
 #pragma unroll
-    for (int ks = -4; ks < 0; ++ks) {
+    for (int ks = -S::kDepth - 1; ks < 0; ++ks) {
       Lp16Step sp;
       dma_plan(ks, sp);
       [&]<int... II>(std::integer_sequence<int, II...>) {
         (S::template dma_a<II>(a_base, a_src, sp.a_pair, sp.a_half, sp.abuf_dma, wave_u), ...);
       }(std::make_integer_sequence<int, NA>{});
-      if (ks >= -3) {
+      if (ks >= -S::kDepth) {
         [&]<int... II>(std::integer_sequence<int, II...>) {
           (S::template dma_b<II>(b_base, b_step, b_src, sp.b_kstep, sp.bbuf_dma, wave_u), ...);
         }(std::make_integer_sequence<int, S::NB>{});
       }
     }
-    // A pair 0 and B step 0 have landed once the two younger steps' loads at most
-    // are outstanding.
+    // A pair 0 and B step 0 have landed once the D - 1 younger steps' loads at
+    // most are outstanding.
     asm volatile("s_waitcnt vmcnt(%0)" ::"i"((S::kBStages - 2) * L) : "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -1161,8 +1169,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_dma16_kernel(
     sp.bst_next = ldsb + (kn % S::kBStages) * S::kBBytes;
     sp.ast_next = lds0 + ((kn / 2) % S::kAStages) * S::kABuf + (kn & 1 ? a_off[1] : a_off[0]);
 
-    // B step ks + 1 (and A's buffer for it) has landed once at most the younger
-    // step's loads are outstanding; the barrier publishes every wave's share and
+    // B step ks + 1 (and A's buffer for it) has landed once at most the D - 2
+    // younger steps' loads are outstanding; the barrier publishes every wave's share and
     // retires the buffers refilled in this step (each wave waited for its reads of
     // them in the step before).  A bare s_barrier: __syncthreads() would drain
     // every outstanding load (vmcnt(0)).
