@@ -32,8 +32,12 @@ against the CPU oracle (ops[*].parity: the GEMM by the reference's 1024-entry sp
 check, the others element by element at BASELINE's tolerances), then times the
 CPU reference of the same GEMM on a bounded row slab (`cpu_baseline`).
 
-Printed: one JSON line (rank 0, N = 1).  `value` is the GEMM's TFLOP/s; `ops` lists
-every kernel with its roofline fraction; `roofline` is the GEMM's.
+Printed: one compact JSON line (rank 0, N = 1, under 4 KB), the last line of
+stdout.  `value` is the GEMM's TFLOP/s; `roofline` is the GEMM's; `ops` holds one
+short row per kernel with its roofline fraction and parity verdict.  The full
+record (every section above, per-op detail, CPU legs) is written beforehand to
+--detail-out (default gpurun_out/bench_detail.json), named in the line's
+`detail_file`.
 """
 from __future__ import annotations
 
@@ -957,14 +961,15 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
       * a 4x4 fan-out of 2048^3 GEMM chains on 4 streams (chain-greedy and
         level-parallel) vs the same graph on one stream, with the overlap (sum of
         node times / wall) and buddy statistics;
-      * the reference graph bench's diamond of 2048^3 GEMMs, its chain of 16
-        bias+GELU nodes on 4096x4096 and its diamond of two grid-starved bias+GELU
-        nodes on 8192x4096, under the three schedules;
+      * the reference graph bench's five graphs at its shapes (mcke_amd.graph.
+        REFERENCE_GRAPHS: diamond of 2048^3 GEMMs, chain of 16 bias+GELU nodes,
+        4x4 fan-out of starved bias+GELU chains, starved diamond, transformer
+        block), under the three schedules, with node sum / wall overlap;
       * for every timed plan the launch-bound ratio (host enqueue time of one
         run / device time of one run, bench/graph_bench.cpp:437-441).
-    At both config-5 shapes it also runs the numerics gate (3 schedules x 3 memory
-    policies x `gate_repeats`, bench/graph_bench.cpp:444-471) and reads every
-    stage of a per-tensor plan back to the host.  Returns (results, verify), where
+    Every one of these graphs also runs the numerics gate (3 schedules x 3 memory
+    policies x `gate_repeats`, bench/graph_bench.cpp:444-471), and every node of
+    a per-tensor plan is read back to the host.  Returns (results, verify), where
     verify(oracle) checks those stages in the CPU leg and stores the outcome under
     results[*]["parity"]."""
     from mcke_amd import graph as G
@@ -1111,71 +1116,72 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
     log(f"config 5 fan-out: numerics gate {'PASS' if gate.passed else 'FAIL'}")
     out["fanout4x4_gemm2048"] = fan
 
-    # The reference graph bench's other topologies (bench/graph_bench.cpp:100-166):
-    # a diamond of 2048^3 GEMMs (B and C from A, D from both), a chain of 16
-    # bias+GELU nodes over X[4096 x 4096], and a diamond whose two middle nodes
-    # are bias+GELU launches starved to 40 workgroup rows, each under the three
-    # schedules.
-    def diamond_gemm(nn):
-        g = G.Graph()
-        a = g.add_input((nn, nn), "A")
-        w = g.add_input((nn, nn), "W")
-        left = g.add_gemm(a, w, "B_gemm")
-        right = g.add_gemm(a, w, "C_gemm")
-        g.mark_output(g.add_gemm(left, right, "D_gemm"))
-        return g, {"A": (a, m.fill_random(nn * nn, 0x4200, -0.0625, 0.0625)),
-                   "W": (w, m.fill_random(nn * nn, 0x4201, -0.0625, 0.0625))}
+    # The reference graph bench's five graphs at its shapes (bench/graph_bench.cpp:
+    # 100-215, run at :477-481): a diamond of 2048^3 GEMMs, a chain of 16 bias+GELU
+    # nodes over X[4096 x 4096], 4 chains of 4 bias+GELU nodes over X[2048 x 2048]
+    # starved to 10 row blocks, a diamond whose middle nodes are bias+GELU starved
+    # to 40 row blocks, and the transformer block (4096, 1024, 4096).  Each is
+    # timed under the three schedules, then run through the numerics gate (3 x 3
+    # x gate_repeats, :444-471), and every node is kept from a per-tensor plan
+    # for the CPU leg's parity check.
+    def numel(g, tid):
+        k = 1
+        for d in g.shape(tid):
+            k *= d
+        return k
 
-    def chain16(rows, cols):
-        g = G.Graph()
-        x = g.add_input((rows, cols), "x")
-        bias = g.add_input((cols,), "bias")
-        cur = x
-        for i in range(16):
-            cur = g.add_bias_act(cur, bias, f"n{i}", act=3)
-        g.mark_output(cur)
-        return g, {"x": (x, m.fill_normal(rows * cols, 0x4300)),
-                   "bias": (bias, m.fill_random(cols, 0x4301, -0.5, 0.5))}
-
-    def diamond_starved(rows, cols, blocks):
-        # B and C: bias+GELU nodes whose grids are capped at `blocks` workgroup rows
-        # (CU-idle but bandwidth-saturated); D joins B's output (graph_bench.cpp:138-153).
-        g = G.Graph()
-        x = g.add_input((rows, cols), "X")
-        bias = g.add_input((cols,), "bias")
-        left = g.add_bias_act(x, bias, "B_starved", act=3, max_row_blocks=blocks)
-        right = g.add_bias_act(x, bias, "C_starved", act=3, max_row_blocks=blocks)
-        g.mark_output(g.add_bias_act(left, bias, "D_join", act=3))
-        g.mark_output(right)
-        return g, {"X": (x, m.fill_normal(rows * cols, 0x4400)),
-                   "bias": (bias, m.fill_random(cols, 0x4401, -0.5, 0.5))}
-
-    ref_graphs = {}
-    for gname, build in (("diamond_gemm_2048", lambda: diamond_gemm(2048)),
-                         ("chain16_4096x4096", lambda: chain16(4096, 4096)),
-                         ("diamond_starved_8192x4096_40", lambda: diamond_starved(8192, 4096, 40))):
+    ref_graphs, ref_nodes = {}, {}
+    for gname in G.REFERENCE_GRAPHS:
         rows = {}
         for label, sched, streams in (("sequential", G.SchedulePolicy.kSequential, 1),
                                       ("level_parallel", G.SchedulePolicy.kLevelParallel, 4),
                                       ("chain_greedy", G.SchedulePolicy.kChainGreedy, 4)):
-            g, inputs = build()
+            g, t, inputs = G.reference_graph(gname, m.fill_random, m.fill_normal)
             ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, schedule=sched,
-                            memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=streams)
+                            memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=streams,
+                            profile=True, profile_slots=warmup + steps)
             ex.plan()
-            for tid, arr in inputs.values():
+            for tid, arr in inputs.items():
                 ex.set_input(tid, arr)
             wall, enq = timed_runs(ex, steps)
+            node_sum = sum(x["median_ms"] for x in ex.timings())
             info = ex.plan_info()
-            rows[label] = {"wall_ms": round(wall, 4), "enqueue_us": round(enq, 2),
+            rows[label] = {"wall_ms": round(wall, 4), "node_sum_ms": round(node_sum, 4),
+                           "overlap": round(node_sum / wall, 3), "enqueue_us": round(enq, 2),
                            "launch_bound_ratio": launch_bound(wall, enq),
                            "streams": info["num_streams_used"], "events": info["num_events"],
+                           "waits": info["waits_dedup"],
                            "arena_bytes": info["arena_bytes"], "naive_bytes": info["naive_bytes"]}
             ex.close()
         for label in ("level_parallel", "chain_greedy"):
             rows[label]["speedup_vs_sequential"] = round(rows["sequential"]["wall_ms"] /
                                                          rows[label]["wall_ms"], 3)
+        # Every node from a per-tensor plan, for the CPU leg.
+        g, t, inputs = G.reference_graph(gname, m.fill_random, m.fill_normal)
+        sizes = {k: numel(g, v) for k, v in t.items() if k != "outs"}
+        ex = G.Executor(g, schedule=G.SchedulePolicy.kSequential,
+                        memory=G.MemoryPolicy.kAllocPerTensor, num_streams=1)
+        ex.plan()
+        for tid, arr in inputs.items():
+            ex.set_input(tid, arr)
+        ex.run_sync()
+        ref_nodes[gname] = (
+            {k: ex.read(v, sizes[k]) for k, v in t.items() if k != "outs" and v not in inputs},
+            {k: inputs[v] for k, v in t.items() if k != "outs" and v in inputs})
+        ex.close()
+        g, t, inputs = G.reference_graph(gname, m.fill_random, m.fill_normal)
+        ex = G.Executor(g, num_streams=4, validate_numerics=True)
+        ex.plan()
+        for tid, arr in inputs.items():
+            ex.set_input(tid, arr)
+        gate = ex.validate_numerics(repeats=gate_repeats)
+        ex.close()
+        rows["gate"] = {"passed": gate.passed, "configs": gate.configs_compared,
+                        "repeats": gate_repeats, "detail": gate.detail}
         ref_graphs[gname] = rows
-        log(f"graph {gname}: " + ", ".join(f"{k} {v['wall_ms']:.3f} ms" for k, v in rows.items()))
+        log(f"graph {gname}: " + ", ".join(f"{k} {v['wall_ms']:.3f} ms" for k, v in rows.items()
+                                          if k != "gate")
+            + f"; numerics gate {'PASS' if gate.passed else 'FAIL'}")
     out["reference_graphs"] = ref_graphs
 
     # Launch-bound shapes: the same MLP chain at small sizes, replayed eagerly (the
@@ -1239,6 +1245,82 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
     fan_cap["same_bits"] = all(np.array_equal(bits_seen[0], b) for b in bits_seen[1:])
     out["fanout_small_capture"] = fan_cap
 
+    # A plan of many short nodes, where one graph launch replaces many eager ones: a
+    # chain of 32 bias+GELU nodes over X[64 x 1024] (256 KiB, about a microsecond
+    # of device work each) on one stream, eager vs replayed.
+    chain_cap = {"shape": "chain of 32 bias+GELU nodes, X[64x1024], 1 stream"}
+    chain_bits = []
+    for label in ("eager", "hip_graph"):
+        g, t = G.chain(32, 64, 1024)
+        ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList,
+                        schedule=G.SchedulePolicy.kSequential,
+                        memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=1)
+        ex.plan()
+        ex.set_input(t["x"], m.fill_normal(64 * 1024, 0x5100))
+        ex.set_input(t["bias"], m.fill_random(1024, 0x5101, -0.5, 0.5))
+        if label == "hip_graph":
+            ex.capture()
+        wall, enq = timed_runs(ex, 200)
+        chain_bits.append(ex.read(t["outs"][0], 64 * 1024).view(np.uint32))
+        chain_cap[label] = {"us_per_run": round(wall * 1e3, 2), "enqueue_us": round(enq, 2)}
+        ex.close()
+    chain_cap["speedup"] = round(chain_cap["eager"]["us_per_run"] /
+                                 chain_cap["hip_graph"]["us_per_run"], 3)
+    chain_cap["same_bits"] = bool(np.array_equal(chain_bits[0], chain_bits[1]))
+    out["chain32_small_capture"] = chain_cap
+    log(f"chain32 64x1024: eager {chain_cap['eager']['us_per_run']} us, hipGraph "
+        f"{chain_cap['hip_graph']['us_per_run']} us per run")
+
+    # The executor's measured choice (capture_if_faster) on each launch-bound plan:
+    # it keeps the graph only where replay beat eager issue on that plan.
+    def choice(build, set_inputs, **kw):
+        g, t = build()
+        ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList,
+                        memory=G.MemoryPolicy.kReuseHappensBefore, **kw)
+        ex.plan()
+        set_inputs(ex, t)
+        d = ex.capture_if_faster(trials=100)
+        ex.close()
+        return {k: (round(v, 2) if isinstance(v, float) else v) for k, v in d.items()}
+
+    def mlp_inputs_small(T2, D2, F2):
+        def f(ex, t):
+            ex.set_input(t["x"], m.fill_normal(T2 * D2, 0x3101, 0.0, 1.0))
+            ex.set_input(t["W1"], m.fill_normal(D2 * F2, 0x3102, 0.0, 0.02))
+            ex.set_input(t["b1"], m.fill_normal(F2, 0x3103, 0.0, 0.01))
+            ex.set_input(t["W2"], m.fill_normal(F2 * D2, 0x3104, 0.0, 0.02))
+            ex.set_input(t["b2"], m.fill_normal(D2, 0x3105, 0.0, 0.01))
+        return f
+
+    def fan_inputs_small(ex, t):
+        ex.set_input(t["W"], m.fill_random(256 * 256, 0x4100, -0.0625, 0.0625))
+        for k, x in enumerate(t["xs"]):
+            ex.set_input(x, m.fill_random(256 * 256, 0x4101 + k))
+
+    def chain_inputs(ex, t):
+        ex.set_input(t["x"], m.fill_normal(64 * 1024, 0x5100))
+        ex.set_input(t["bias"], m.fill_random(1024, 0x5101, -0.5, 0.5))
+
+    out["capture_choice"] = {
+        "mlp_512x256x1024_2streams": choice(lambda: G.mlp_block(512, 256, 1024),
+                                            mlp_inputs_small(512, 256, 1024),
+                                            schedule=G.SchedulePolicy.kChainGreedy, num_streams=2),
+        "mlp_64x64x256_2streams": choice(lambda: G.mlp_block(64, 64, 256),
+                                         mlp_inputs_small(64, 64, 256),
+                                         schedule=G.SchedulePolicy.kChainGreedy, num_streams=2),
+        "fanout_4x4_256_4streams": choice(lambda: G.gemm_fanout(4, 4, 256), fan_inputs_small,
+                                          schedule=G.SchedulePolicy.kChainGreedy, num_streams=4),
+        "chain32_64x1024_1stream": choice(lambda: G.chain(32, 64, 1024), chain_inputs,
+                                          schedule=G.SchedulePolicy.kSequential, num_streams=1),
+    }
+    for k, v in out["capture_choice"].items():
+        log(f"capture_if_faster {k}: eager {v['eager_us_per_run']} us, replay "
+            f"{v['replay_us_per_run']} us -> {'graph' if v['captured'] else 'eager'}")
+
+    out["gates_passed"] = bool(out["mlp_block"]["gate"]["passed"] and
+                               out["fanout4x4_gemm2048"]["gate"]["passed"] and
+                               all(r["gate"]["passed"] for r in ref_graphs.values()))
+
     def verify(orc):
         from oracle import graph_checks as gc
         mlp = gc.check_mlp(mlp_in, host["mlp"], T, D, F)
@@ -1247,7 +1329,27 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
         fp = gc.check_fanout(fan_w, fan_xs, host["fan"], fan_n)
         fp["ok"] = bool(fp["ok"] and out["fanout4x4_gemm2048"]["gate"]["passed"])
         out["fanout4x4_gemm2048"]["parity"] = fp
-        return {"ok": mlp["ok"] and fp["ok"]}
+        ok = mlp["ok"] and fp["ok"]
+        for gname, (nodes, inp) in ref_nodes.items():
+            if gname == "diamond_gemm_2048":
+                r = gc.check_diamond_gemm(inp["A"], inp["W"], nodes, 2048)
+            elif gname == "chain16":
+                r = gc.check_bias_chain(inp["x"], inp["bias"], [nodes[f"n{i}"] for i in range(16)],
+                                        4096, 4096)
+            elif gname == "fanout4x4":
+                r = {f"b{k}": gc.check_bias_chain(inp["x"], inp["bias"],
+                                                  [nodes[f"b{k}n{d}"] for d in range(4)], 2048, 2048)
+                     for k in range(4)}
+                r["ok"] = all(v["ok"] for v in r.values())
+            elif gname == "diamond_starved":
+                r = gc.check_diamond_starved(inp["X"], inp["bias"], nodes, 8192, 4096)
+            else:
+                r = gc.check_transformer(inp, nodes, 4096, 1024, 4096)
+            r["ok"] = bool(r["ok"] and ref_graphs[gname]["gate"]["passed"])
+            ref_graphs[gname]["parity"] = {"ok": r["ok"]}
+            ok = ok and r["ok"]
+        ref_nodes.clear()
+        return {"ok": bool(ok)}
 
     return out, verify
 
@@ -1382,6 +1484,72 @@ def cpu_baseline(m, gemm_bufs, ops, seconds_target=10.0, stream=None, runs=5):
     }
 
 
+HEADLINE_MAX_BYTES = 4096
+
+
+def headline(detail: dict, detail_file: str | None) -> dict:
+    """The compact record printed as stdout's last line: the contract fields, the
+    GEMM's roofline, the CPU baseline's summary and one short row per op, in the
+    spirit of the reference's one-CSV-row-per-kernel profiler record
+    (src/core/profiler.cpp:95-113).  Every other section stays in `detail`, which
+    bench.py writes to `detail_file`.  Kept under HEADLINE_MAX_BYTES: extra keys
+    are dropped, least important first, until it fits."""
+    keep = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+            "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config", "roofline")
+    line = {k: detail.get(k) for k in keep}
+    cpu = detail.get("cpu_baseline")
+    if cpu:
+        line["cpu_baseline"] = {
+            "value": cpu.get("value"), "unit": cpu.get("unit"), "cores": cpu.get("cores"),
+            "kind": cpu.get("kind"), "sample": cpu.get("sample"),
+            "extrapolated_8192_s": cpu.get("extrapolated_8192_s"),
+            "parity_ok": (cpu.get("parity_on_sample") or {}).get("ok"),
+            "ops_gb_s": {r["name"]: r["gb_s"] for r in cpu.get("ops", [])},
+        }
+    else:
+        line["cpu_baseline"] = None
+    # One row per op: [name, avg_ms, achieved, unit, frac of the published peak, parity ok].
+    line["ops"] = [[s["name"], s["avg_ms"], s["achieved"], s["unit"], s["frac"],
+                    (s.get("parity") or {}).get("ok")] for s in detail.get("ops") or []]
+    line["ops_columns"] = ["name", "avg_ms", "achieved", "unit", "frac", "parity_ok"]
+    extra = {}
+    peaks = detail.get("measured_peaks")
+    if peaks:
+        extra["measured_peaks"] = {k: peaks[k] for k in
+                                   ("mfma_f32_tflops", "stream_triad_gb_s", "stream_copy_gb_s",
+                                    "stream_copy_32mib_gb_s") if k in peaks}
+    sweep = detail.get("gemm_sweep") or []
+    if sweep:
+        extra["gemm_sweep_tflops"] = {str(r["n"]): [r["mfma"]["tflops"], r["rocblas"]["tflops"]]
+                                      for r in sweep}
+    lp = detail.get("gemm_lp") or {}
+    if lp.get("runs"):
+        extra["gemm_lp_tflops"] = {f"{r['ab']}->{r['c']} {r['n']}": r["tflops"]
+                                   for r in lp["runs"]}
+    graph = detail.get("graph") or {}
+    if graph.get("mlp_block"):
+        g = graph["mlp_block"]
+        extra["graph_mlp"] = {"wall_ms": g.get("wall_ms"), "tflops": g.get("tflops"),
+                              "bound_over_wall": g.get("bound_over_wall")}
+    if graph.get("gates_passed") is not None:
+        extra["graph_gates_passed"] = graph["gates_passed"]
+    if graph.get("capture_choice"):
+        # Per launch-bound plan: [eager us, replay us, graph kept].
+        extra["graph_capture_choice"] = {
+            k: [v["eager_us_per_run"], v["replay_us_per_run"], v["captured"]]
+            for k, v in graph["capture_choice"].items()}
+    parity = [s.get("parity", {}).get("ok") for s in detail.get("ops") or [] if s.get("parity")]
+    extra["all_parity_ok"] = all(parity) if parity else None
+    extra["detail_file"] = detail_file
+    line.update(extra)
+    for k in ("graph_capture_choice", "graph_mlp", "gemm_lp_tflops", "gemm_sweep_tflops",
+              "measured_peaks", "data"):
+        if len(json.dumps(line, separators=(",", ":"))) <= HEADLINE_MAX_BYTES:
+            break
+        line.pop(k, None)
+    return line
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -1401,6 +1569,9 @@ def main(argv=None) -> int:
     p.add_argument("--only", default=None,
                    help="comma-separated op-name prefixes to run (profiling); enables "
                         "the copy_256mib calibration op")
+    p.add_argument("--detail-out", default=os.path.join(ROOT, "gpurun_out", "bench_detail.json"),
+                   help="file that receives the full record (every section); stdout's last "
+                        "line carries the compact headline")
     args = p.parse_args(argv)
     only = set(args.only.split(",")) if args.only else None
 
@@ -1495,7 +1666,7 @@ def main(argv=None) -> int:
     gemm = summaries[0] if summaries else {"achieved": None, "unit": None, "bound": None,
                                            "peak": None, "frac": None, "name": None}
 
-    line = {
+    detail = {
         "metric": METRIC,
         "value": gemm["achieved"],
         "unit": gemm["unit"],
@@ -1530,7 +1701,15 @@ def main(argv=None) -> int:
         "graph": graph_res,
         "ladder": ladder_res,
     }
-    print(json.dumps(line), flush=True)
+    # The full record goes to a file first; stdout's last line is the compact
+    # headline, which must stay whole inside the few KB of stdout a driver keeps.
+    detail_path = os.path.abspath(args.detail_out)
+    os.makedirs(os.path.dirname(detail_path), exist_ok=True)
+    with open(detail_path, "w") as f:
+        json.dump(detail, f, indent=1)
+    log(f"full record ({os.path.getsize(detail_path)} bytes) written to {detail_path}")
+    line = headline(detail, os.path.relpath(detail_path, ROOT))
+    print(json.dumps(line, separators=(",", ":")), flush=True)
     del keep
     return 0
 

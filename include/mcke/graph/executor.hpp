@@ -58,6 +58,14 @@ struct NumericsResult {
   std::string detail;
 };
 
+// What capture_if_faster() measured and kept (no reference counterpart).
+struct CaptureDecision {
+  bool captured = false;          // the graph was kept: run_async() replays it
+  double eager_us_per_run = 0.0;  // best block, host wall time per run issued eagerly
+  double replay_us_per_run = 0.0; // best block, host wall time per replayed run
+  int trials = 0;                 // runs per block (two blocks each way, alternating)
+};
+
 struct NodeTiming {
   NodeId node = kInvalidNode;
   std::string name;
@@ -155,6 +163,16 @@ class GraphExecutor {
   // iteration's.  plan() drops the captured graph, since it binds the old plan's
   // buffers.
   [[nodiscard]] Status capture_graph();
+  // capture_graph(), then keep the graph only where replay measures faster than
+  // eager issue on this plan.  A replay costs a fixed host time per graph launch
+  // on this runtime, a few microseconds, where eager issue costs a little per
+  // node: replay pays for plans of many short nodes and loses on plans of a few.
+  // So the choice is measured: `trials` back-to-back runs eagerly, then
+  // `trials` replayed, twice in alternation, each block timed on the host from
+  // its first enqueue to its last run's completion; the best block of each
+  // decides.  A losing graph is released, and run_async() issues the plan's
+  // launches as before.  Outputs are the same bits either way.
+  [[nodiscard]] StatusOr<CaptureDecision> capture_if_faster(int trials = 50);
   [[nodiscard]] bool captured() const noexcept { return replay_ != nullptr; }
   [[nodiscard]] Status synchronize();
   [[nodiscard]] Status run_sync() {

@@ -137,6 +137,14 @@ int mcke_executor_synchronize(mcke_executor* e);
  * per-node timing probes or a vendor-library GEMM node.  A new plan() drops the
  * capture. */
 int mcke_executor_capture(mcke_executor* e);
+/* No reference counterpart (the reference plans capture to cut per-launch host
+ * cost, executor.hpp:23-27): captures as mcke_executor_capture, then keeps the
+ * graph only if replay measures faster than eager issue on this plan -- `trials`
+ * runs each way, twice in alternation, host wall time per run of the best block
+ * (GraphExecutor::capture_if_faster).  *captured (may be NULL) is 1 when the graph
+ * was kept; *eager_us and *replay_us (may be NULL) receive the two times. */
+int mcke_executor_capture_if_faster(mcke_executor* e, int trials, int* captured, double* eager_us,
+                                    double* replay_us);
 int mcke_executor_is_captured(mcke_executor* e, int* out);
 /* Copies tensor t (an output, or any tensor with a buffer) to host memory and waits. */
 int mcke_executor_read_tensor(mcke_executor* e, uint32_t t, void* host, size_t bytes);

@@ -224,8 +224,13 @@ int launch_fused_vw(const float* x, const float* bias, float* y, int64_t rows, i
 template <int VW>
 int launch_act_vw(const float* x, float* y, int64_t n, int act, hipStream_t s) {
   const int64_t n_v = n / VW;
+  // The launch's global work size (blocks x kRowLanes) must fit 32 bits; 2^24
+  // one-wave workgroups (2^30 lanes) stay below that and still fill the chip many
+  // times over, and the kernel's grid-stride loop covers any n_v beyond them.
+  constexpr int64_t kMaxBlocks = int64_t{1} << 24;
+  static_assert(kMaxBlocks * kRowLanes <= (int64_t{1} << 32) - 1, "global work size fits 32 bits");
   int64_t blocks = (n_v + kRowLanes - 1) / kRowLanes;
-  if (blocks > (1 << 30)) blocks = 1 << 30;
+  if (blocks > kMaxBlocks) blocks = kMaxBlocks;
   const unsigned g = static_cast<unsigned>(blocks);
   constexpr int L = kRowLanes;
   switch (act) {

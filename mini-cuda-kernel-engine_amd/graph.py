@@ -111,6 +111,8 @@ def host_lib() -> C.CDLL:
         "mcke_executor_run_async": (C.c_int, [_VP]),
         "mcke_executor_synchronize": (C.c_int, [_VP]),
         "mcke_executor_capture": (C.c_int, [_VP]),
+        "mcke_executor_capture_if_faster": (C.c_int, [_VP, C.c_int, C.POINTER(C.c_int),
+                                                      C.POINTER(C.c_double), C.POINTER(C.c_double)]),
         "mcke_executor_is_captured": (C.c_int, [_VP, C.POINTER(C.c_int)]),
         "mcke_executor_read_tensor": (C.c_int, [_VP, _U32, _VP, C.c_size_t]),
         "mcke_executor_plan_info": (C.c_int, [_VP, C.POINTER(PlanInfo)]),
@@ -261,6 +263,15 @@ class Executor:
         """Capture one iteration into a HIP graph; later run_async() replays it."""
         _check(host_lib().mcke_executor_capture(self.h))
 
+    def capture_if_faster(self, trials: int = 50) -> dict:
+        """Capture, then keep the HIP graph only if replay measures faster than eager
+        issue on this plan (GraphExecutor::capture_if_faster)."""
+        cap, e_us, r_us = C.c_int(0), C.c_double(0.0), C.c_double(0.0)
+        _check(host_lib().mcke_executor_capture_if_faster(self.h, trials, C.byref(cap), C.byref(e_us),
+                                                          C.byref(r_us)))
+        return {"captured": bool(cap.value), "eager_us_per_run": e_us.value,
+                "replay_us_per_run": r_us.value, "trials": trials}
+
     @property
     def captured(self) -> bool:
         out = C.c_int(0)
@@ -359,3 +370,124 @@ def gemm_fanout(branches: int, depth: int, n: int, gemm_variant=GemmVariant.kMfm
         outs.append(cur)
         nodes.append(chain)
     return g, {"W": w, "xs": xs, "outs": outs, "nodes": nodes}
+
+
+# ---------------------------------------------------------------------------
+# The reference graph bench's five topologies (bench/graph_bench.cpp:100-215, run at
+# :477-481).  Each returns (graph, tensors): the graph's inputs, every node's output
+# under its node name and "outs", the graph outputs.  Activations are GELU_tanh as
+# in the reference's bias_act_op (:91-96).  GEMM nodes run this build's kMfmaF32
+# kernel with the tile picked per shape, where the reference's run its
+# register-blocked FFMA kernel (gemm_op, :85-90).
+# ---------------------------------------------------------------------------
+
+def diamond_gemm(n: int):
+    """B = A W and C = A W, then D = B C (graph_bench.cpp:100-113)."""
+    g = Graph()
+    a = g.add_input((n, n), "A")
+    w = g.add_input((n, n), "W")
+    left = g.add_gemm(a, w, "B_gemm")
+    right = g.add_gemm(a, w, "C_gemm")
+    d = g.add_gemm(left, right, "D_gemm")
+    g.mark_output(d)
+    return g, {"A": a, "W": w, "B_gemm": left, "C_gemm": right, "D_gemm": d, "outs": [d]}
+
+
+def chain(nodes: int, rows: int, cols: int):
+    """`nodes` bias+GELU nodes in a row over x[rows x cols], all with one bias
+    (graph_bench.cpp:155-171)."""
+    g = Graph()
+    x = g.add_input((rows, cols), "x")
+    bias = g.add_input((cols,), "bias")
+    t = {"x": x, "bias": bias}
+    cur = x
+    for i in range(nodes):
+        cur = g.add_bias_act(cur, bias, f"n{i}", act=3)
+        t[f"n{i}"] = cur
+    g.mark_output(cur)
+    t["outs"] = [cur]
+    return g, t
+
+
+def fanout(branches: int, depth: int, rows: int, cols: int, max_row_blocks: int):
+    """`branches` chains of `depth` bias+GELU nodes, every chain starting from x and
+    every node's grid capped at `max_row_blocks` row blocks (graph_bench.cpp:173-194;
+    the reference benches fanout(4, 4, 2048, 2048, 10)).  Node d of chain k is
+    "b{k}n{d}"."""
+    g = Graph()
+    x = g.add_input((rows, cols), "x")
+    bias = g.add_input((cols,), "bias")
+    t = {"x": x, "bias": bias, "outs": []}
+    for k in range(branches):
+        cur = x
+        for d in range(depth):
+            cur = g.add_bias_act(cur, bias, f"b{k}n{d}", act=3, max_row_blocks=max_row_blocks)
+            t[f"b{k}n{d}"] = cur
+        g.mark_output(cur)
+        t["outs"].append(cur)
+    return g, t
+
+
+def diamond_starved(rows: int, cols: int, max_row_blocks: int):
+    """B and C: bias+GELU of X with grids capped at `max_row_blocks` row blocks; D:
+    bias+GELU of B, uncapped; outputs D and C (graph_bench.cpp:138-153)."""
+    g = Graph()
+    x = g.add_input((rows, cols), "X")
+    bias = g.add_input((cols,), "bias")
+    left = g.add_bias_act(x, bias, "B_starved", act=3, max_row_blocks=max_row_blocks)
+    right = g.add_bias_act(x, bias, "C_starved", act=3, max_row_blocks=max_row_blocks)
+    d = g.add_bias_act(left, bias, "D_join", act=3)
+    g.mark_output(d)
+    g.mark_output(right)
+    return g, {"X": x, "bias": bias, "B_starved": left, "C_starved": right, "D_join": d,
+               "outs": [d, right]}
+
+
+def transformer_block(tokens: int, d_model: int, d_ff: int):
+    """GEMM -> bias+GELU -> GEMM -> row softmax, no second bias
+    (graph_bench.cpp:199-215; benched at (4096, 1024, 4096))."""
+    g = Graph()
+    x = g.add_input((tokens, d_model), "x")
+    w1 = g.add_input((d_model, d_ff), "W1")
+    b1 = g.add_input((d_ff,), "b1")
+    w2 = g.add_input((d_ff, d_model), "W2")
+    g1 = g.add_gemm(x, w1, "gemm1")
+    h = g.add_bias_act(g1, b1, "bias_gelu", act=3)
+    g2 = g.add_gemm(h, w2, "gemm2")
+    y = g.add_softmax(g2, "softmax")
+    g.mark_output(y)
+    return g, {"x": x, "W1": w1, "b1": b1, "W2": w2, "gemm1": g1, "bias_gelu": h, "gemm2": g2,
+               "softmax": y, "outs": [y]}
+
+
+# name -> (builder, {input name: ("u", seed, lo, hi) | ("n", seed, mean, sigma)}): the
+# five graphs the reference's graph bench runs, at its shapes (graph_bench.cpp:477-481),
+# with seeded inputs drawn by fill_random (U[lo, hi)) or fill_normal (N(mean, sigma^2)).
+REFERENCE_GRAPHS = {
+    "diamond_gemm_2048": (lambda: diamond_gemm(2048),
+                          {"A": ("u", 0x4200, -0.0625, 0.0625), "W": ("u", 0x4201, -0.0625, 0.0625)}),
+    "chain16": (lambda: chain(16, 4096, 4096),
+                {"x": ("n", 0x4300, 0.0, 1.0), "bias": ("u", 0x4301, -0.5, 0.5)}),
+    "fanout4x4": (lambda: fanout(4, 4, 2048, 2048, 10),
+                  {"x": ("n", 0x4600, 0.0, 1.0), "bias": ("u", 0x4601, -0.5, 0.5)}),
+    "diamond_starved": (lambda: diamond_starved(8192, 4096, 40),
+                        {"X": ("n", 0x4400, 0.0, 1.0), "bias": ("u", 0x4401, -0.5, 0.5)}),
+    "transformer_block": (lambda: transformer_block(4096, 1024, 4096),
+                          {"x": ("n", 0x4500, 0.0, 1.0), "W1": ("n", 0x4501, 0.0, 0.02),
+                           "b1": ("n", 0x4502, 0.0, 0.01), "W2": ("n", 0x4503, 0.0, 0.02)}),
+}
+
+
+def reference_graph(name: str, fill_random, fill_normal):
+    """(graph, tensors, {tensor id: host input}) for REFERENCE_GRAPHS[name], the
+    inputs drawn with the given generators (the package's or the oracle's, which
+    give the same bits)."""
+    build, spec = REFERENCE_GRAPHS[name]
+    g, t = build()
+    inputs = {}
+    for key, (kind, seed, p0, p1) in spec.items():
+        n = 1
+        for d in g.shape(t[key]):
+            n *= d
+        inputs[t[key]] = fill_random(n, seed, p0, p1) if kind == "u" else fill_normal(n, seed, p0, p1)
+    return g, t, inputs

@@ -15,6 +15,7 @@
 #include "mcke/graph/executor.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 #include <sstream>
 
@@ -316,6 +317,40 @@ Status GraphExecutor::capture_graph() {
   MCKE_RETURN_IF_ERROR(from_abi(mcke_rt_graph_upload(replay_, plan_.lanes_.front().native()),
                                 "capture_graph: upload"));
   return plan_.lanes_.front().synchronize();
+}
+
+StatusOr<CaptureDecision> GraphExecutor::capture_if_faster(int trials) {
+  if (trials < 1) return InvalidArgumentError("capture_if_faster: trials must be >= 1");
+  MCKE_RETURN_IF_ERROR(capture_graph());
+  void* graph = replay_;
+  // One block: `trials` runs back to back, host wall time per run from the first
+  // enqueue to the completion of the last.
+  auto block = [&](void* use) -> StatusOr<double> {
+    replay_ = use;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < trials; ++r) MCKE_RETURN_IF_ERROR(run_async());
+    MCKE_RETURN_IF_ERROR(synchronize());
+    const auto t1 = std::chrono::steady_clock::now();
+    return std::chrono::duration<double, std::micro>(t1 - t0).count() / trials;
+  };
+  CaptureDecision d;
+  d.trials = trials;
+  d.eager_us_per_run = d.replay_us_per_run = 1e300;
+  for (int round = 0; round < 2; ++round) {
+    auto e = block(nullptr);
+    if (!e.ok()) {
+      replay_ = graph;
+      return e.status();
+    }
+    auto g = block(graph);
+    if (!g.ok()) return g.status();
+    d.eager_us_per_run = std::min(d.eager_us_per_run, *e);
+    d.replay_us_per_run = std::min(d.replay_us_per_run, *g);
+  }
+  replay_ = graph;
+  d.captured = d.replay_us_per_run < d.eager_us_per_run;
+  if (!d.captured) drop_replay();
+  return d;
 }
 
 // Several streams: no capture may span two of them, so each node's launches are

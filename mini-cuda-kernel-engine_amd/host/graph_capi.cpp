@@ -211,6 +211,17 @@ int mcke_executor_synchronize(mcke_executor* e) { return e ? code(e->exec->synch
 
 int mcke_executor_capture(mcke_executor* e) { return e ? code(e->exec->capture_graph()) : bad("null executor"); }
 
+int mcke_executor_capture_if_faster(mcke_executor* e, int trials, int* captured, double* eager_us,
+                                    double* replay_us) {
+  if (!e) return bad("null executor");
+  auto d = e->exec->capture_if_faster(trials);
+  if (!d.ok()) return code(d.status());
+  if (captured) *captured = d->captured ? 1 : 0;
+  if (eager_us) *eager_us = d->eager_us_per_run;
+  if (replay_us) *replay_us = d->replay_us_per_run;
+  return MCKE_STATUS_OK;
+}
+
 int mcke_executor_is_captured(mcke_executor* e, int* out) {
   if (!e || !out) return bad("mcke_executor_is_captured: null argument");
   *out = e->exec->captured() ? 1 : 0;

@@ -1,5 +1,5 @@
 """Stage-wise checks of BASELINE config 5 -- the MLP block and the GEMM fan-out --
-against the CPU oracle.  Test infrastructure: imported only by tests/ and by
+and of the reference graph bench's five topologies against the CPU oracle.  Test infrastructure: imported only by tests/ and by
 bench.py's CPU leg, as the checker of what the GPU computed.
 
 Every node is checked on the GPU's own input to that node (read back from a
@@ -92,5 +92,56 @@ def check_fanout(w, xs: list, nodes: list, n: int) -> dict:
         for d, got in enumerate(chain):
             res[f"b{k}g{d}"] = check_gemm(cur, w, got, n, n, n)
             cur = got
+    res["ok"] = all(v["ok"] for v in res.values())
+    return res
+
+
+def check_bias_chain(x, bias, outs: list, rows: int, cols: int, act: int = 3) -> dict:
+    """outs[d]: the GPU's output of bias+act node d of a chain whose input is x
+    (d = 0) or outs[d - 1] -- one chain of the reference's `chain` and `fanout`
+    graphs (bench/graph_bench.cpp:155-194)."""
+    res, cur = {}, x
+    for d, got in enumerate(outs):
+        res[f"n{d}"] = check_bias_act(cur, bias, got, rows, cols, act)
+        cur = got
+    res["ok"] = all(v["ok"] for v in res.values())
+    return res
+
+
+def check_transformer(inp: dict, stages: dict, T: int, D: int, F: int) -> dict:
+    """The reference's transformer_block (bench/graph_bench.cpp:199-215): inp holds
+    x [T x D], W1 [D x F], b1 [F], W2 [F x D]; stages the GPU's gemm1 [T x F],
+    bias_gelu [T x F], gemm2 [T x D] and softmax [T x D]."""
+    res = {
+        "gemm1": check_gemm(inp["x"], inp["W1"], stages["gemm1"], T, F, D),
+        "bias_gelu": check_bias_act(stages["gemm1"], inp["b1"], stages["bias_gelu"], T, F, 3),
+        "gemm2": check_gemm(stages["bias_gelu"], inp["W2"], stages["gemm2"], T, D, F),
+        "softmax": check_softmax(stages["gemm2"], stages["softmax"], T, D),
+    }
+    res["ok"] = all(v["ok"] for v in res.values())
+    return res
+
+
+def check_diamond_gemm(a, w, stages: dict, n: int) -> dict:
+    """B = A W, C = A W, D = B C (bench/graph_bench.cpp:100-113) on the GPU's B and C."""
+    res = {
+        "B_gemm": check_gemm(a, w, stages["B_gemm"], n, n, n),
+        "C_gemm": check_gemm(a, w, stages["C_gemm"], n, n, n),
+        "D_gemm": check_gemm(stages["B_gemm"], stages["C_gemm"], stages["D_gemm"], n, n, n),
+    }
+    # B and C are the same product of the same operands under the same kernel.
+    res["B_equals_C_bitwise"] = {"ok": bool(np.array_equal(
+        np.asarray(stages["B_gemm"]).view(np.uint32), np.asarray(stages["C_gemm"]).view(np.uint32)))}
+    res["ok"] = all(v["ok"] for v in res.values())
+    return res
+
+
+def check_diamond_starved(x, bias, stages: dict, rows: int, cols: int) -> dict:
+    """B and C = bias+GELU(X), D = bias+GELU(B) (bench/graph_bench.cpp:138-153)."""
+    res = {
+        "B_starved": check_bias_act(x, bias, stages["B_starved"], rows, cols, 3),
+        "C_starved": check_bias_act(x, bias, stages["C_starved"], rows, cols, 3),
+        "D_join": check_bias_act(stages["B_starved"], bias, stages["D_join"], rows, cols, 3),
+    }
     res["ok"] = all(v["ok"] for v in res.values())
     return res

@@ -59,11 +59,16 @@ def _quarters(rng, shape):
     return (rng.integers(-8, 9, size=shape) / 4.0).astype(np.float32)
 
 
-# The last four are whole tiles for the direct-to-LDS kernel with 1, 3, 5 and 7
-# K steps of 32 (its 4-stage ring's prologue and tail).
+# Whole tiles for the direct-to-LDS kernels (tiles with BN >= 128):
+#   * K % 64 == 32 takes the 32x32x16 kernel; K = 32, 96, 160, 224 give it 1, 3, 5
+#     and 7 K steps of 32 (its 4-stage ring's prologue and tail);
+#   * K % 64 == 0 takes the 16x16x32 kernel, whose ring is 3 steps deep and clamps
+#     the A pair and B step it fetches past the end; K = 64, 128, 192, 320 give it
+#     2, 4, 6 and 10 steps (K = 64: fewer steps than the ring is deep).
 QSHAPES = [(1, 1, 1), (5, 7, 3), (129, 65, 257), (1, 64, 128), (64, 1, 128), (33, 63, 1),
            (253, 253, 253), (256, 256, 256), (512, 512, 512),
-           (256, 256, 32), (256, 256, 96), (256, 512, 160), (512, 256, 224)]
+           (256, 256, 32), (256, 256, 96), (256, 512, 160), (512, 256, 224),
+           (256, 256, 64), (256, 512, 128), (512, 256, 192), (256, 256, 320)]
 
 
 @pytest.mark.parametrize("dt", DTS, ids=DT_ID.get)

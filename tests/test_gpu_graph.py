@@ -483,3 +483,58 @@ def test_captured_split_reduce_replays(G, orc):
             r = orc.compare(got, want, 1e-5, floor)
             assert r.ok, f"replay {rep} kind {kind}: {r}"
     ex.close()
+
+
+@pytest.mark.parametrize("plan", ["mlp_64x64x256_2streams", "chain32_64x1024_1stream",
+                                  "fanout_4x4_256_4streams"])
+def test_capture_if_faster_keeps_the_faster_path(G, orc, plan):
+    """capture_if_faster measures eager issue against graph replay on the plan and
+    keeps the graph only where replay was faster; either way the executor's
+    outputs are the eager bits, before and after the choice, over several runs."""
+    if plan.startswith("mlp"):
+        T, D, F = 64, 64, 256
+        g, t = G.mlp_block(T, D, F)
+        kw = dict(schedule=G.SchedulePolicy.kChainGreedy, num_streams=2)
+        inputs = {t[k]: v for k, v in _mlp_inputs(orc, T, D, F).items()}
+        outs = [(t["y"], T * D)]
+        build = lambda: G.mlp_block(T, D, F)  # noqa: E731
+    elif plan.startswith("chain"):
+        build = lambda: G.chain(32, 64, 1024)  # noqa: E731
+        g, t = build()
+        kw = dict(schedule=G.SchedulePolicy.kSequential, num_streams=1)
+        inputs = {t["x"]: orc.fill_normal(64 * 1024, 0x5100), t["bias"]: orc.fill_random(1024, 0x5101, -0.5, 0.5)}
+        outs = [(t["outs"][0], 64 * 1024)]
+    else:
+        n = 256
+        build = lambda: G.gemm_fanout(4, 4, n)  # noqa: E731
+        g, t = build()
+        kw = dict(schedule=G.SchedulePolicy.kChainGreedy, num_streams=4)
+        inputs = {t["W"]: orc.fill_random(n * n, 0x4100, -0.0625, 0.0625)}
+        inputs.update({x: orc.fill_random(n * n, 0x4101 + k) for k, x in enumerate(t["xs"])})
+        outs = [(o, n * n) for o in t["outs"]]
+
+    def run(ex):
+        ex.run_sync()
+        return [ex.read(o, k).view(np.uint32) for o, k in outs]
+
+    ref = G.Executor(g, **kw)
+    ref.plan()
+    for tid, arr in inputs.items():
+        ref.set_input(tid, arr)
+    gold = run(ref)
+    ref.close()
+
+    g, t2 = build()
+    ex = G.Executor(g, **kw)
+    ex.plan()
+    for tid, arr in inputs.items():
+        ex.set_input(tid, arr)
+    d = ex.capture_if_faster(trials=40)
+    print(plan, d)
+    assert d["eager_us_per_run"] > 0 and d["replay_us_per_run"] > 0
+    assert d["captured"] == (d["replay_us_per_run"] < d["eager_us_per_run"])
+    assert ex.captured == d["captured"]
+    for rep in range(3):
+        for got, want in zip(run(ex), gold):
+            assert np.array_equal(got, want), f"{plan} run {rep} (captured={d['captured']})"
+    ex.close()

@@ -1,0 +1,120 @@
+"""The reference graph bench's five graphs (bench/graph_bench.cpp:100-215, run at
+:477-481) at its shapes, through GraphExecutor on the GPU:
+
+  diamond_gemm_2048   B = A W, C = A W, D = B C, 2048^3 GEMMs
+  chain16             16 bias+GELU nodes over x[4096 x 4096]
+  fanout4x4           4 chains of 4 bias+GELU nodes over x[2048 x 2048], grids
+                      capped at 10 row blocks
+  diamond_starved     bias+GELU of X[8192 x 4096] at 40 row blocks, twice, then a
+                      join node
+  transformer_block   GEMM [4096 x 1024 x 4096] -> bias+GELU -> GEMM -> softmax
+
+For each: every node checked on its own GPU input against the CPU oracle from a
+sequential per-tensor plan (oracle/graph_checks.py: GEMMs by the reference's
+1024-entry spot check, bias+GELU element by element at abs 1e-6 + rel 1e-6,
+softmax at abs 1e-6 with row sums within 1e-5); the plan bench.py times
+(chain-greedy, 4 streams, arena shared under happens-before, buddy allocator)
+giving the same output bits; and the numerics gate (3 schedules x 3 memory
+policies, bitwise identical over repeats), as the reference's graph bench gates
+every graph it times (:444-471)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GRAPHS = ["diamond_gemm_2048", "chain16", "fanout4x4", "diamond_starved", "transformer_block"]
+
+
+@pytest.fixture(scope="module")
+def G(gpu):
+    from mcke_amd import graph
+    return graph
+
+
+@pytest.fixture(scope="module")
+def checks(orc):
+    from oracle import graph_checks
+    return graph_checks
+
+
+def _numel(g, t):
+    n = 1
+    for d in g.shape(t):
+        n *= d
+    return n
+
+
+def _executor(G, name, orc, **kw):
+    g, t, inputs = G.reference_graph(name, orc.fill_random, orc.fill_normal)
+    sizes = {k: _numel(g, v) for k, v in t.items() if k != "outs"}
+    outs = list(t["outs"])
+    ex = G.Executor(g, **kw)
+    ex.plan()
+    for tid, arr in inputs.items():
+        ex.set_input(tid, arr)
+    return ex, t, sizes, outs, inputs
+
+
+def _host_inputs(t, inputs):
+    return {k: inputs[v] for k, v in t.items() if k != "outs" and v in inputs}
+
+
+def _check(checks, name, t, host, inp):
+    if name == "diamond_gemm_2048":
+        return checks.check_diamond_gemm(inp["A"], inp["W"], host, 2048)
+    if name == "chain16":
+        return checks.check_bias_chain(inp["x"], inp["bias"], [host[f"n{i}"] for i in range(16)],
+                                       4096, 4096)
+    if name == "fanout4x4":
+        res = {f"b{k}": checks.check_bias_chain(inp["x"], inp["bias"],
+                                                [host[f"b{k}n{d}"] for d in range(4)], 2048, 2048)
+               for k in range(4)}
+        res["ok"] = all(v["ok"] for v in res.values())
+        return res
+    if name == "diamond_starved":
+        return checks.check_diamond_starved(inp["X"], inp["bias"], host, 8192, 4096)
+    return checks.check_transformer(inp, host, 4096, 1024, 4096)
+
+
+@pytest.mark.parametrize("name", GRAPHS)
+def test_reference_graph_every_node_and_timed_plan_bits(G, orc, checks, name):
+    print(f"reference graph {name}: per-tensor plan", flush=True)
+    ex, t, sizes, outs, inputs = _executor(G, name, orc, schedule=G.SchedulePolicy.kSequential,
+                                           memory=G.MemoryPolicy.kAllocPerTensor, num_streams=1)
+    ex.run_sync()
+    node_keys = [k for k in t if k != "outs" and t[k] not in inputs]
+    host = {k: ex.read(t[k], sizes[k]) for k in node_keys}
+    want_out = [ex.read(o, _numel_of(sizes, t, o)) for o in outs]
+    ex.close()
+    res = _check(checks, name, t, host, _host_inputs(t, inputs))
+    assert res["ok"], res
+
+    print(f"reference graph {name}: timed plan", flush=True)
+    ex, t2, _, outs2, _ = _executor(G, name, orc, allocator=G.AllocatorKind.kBuddy,
+                                    schedule=G.SchedulePolicy.kChainGreedy,
+                                    memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4)
+    for _ in range(2):
+        ex.run_sync()
+        for o, w in zip(outs2, want_out):
+            got = ex.read(o, w.size)
+            assert np.array_equal(got.view(np.uint32), w.view(np.uint32)), name
+    ex.close()
+
+
+def _numel_of(sizes, t, tid):
+    for k, v in t.items():
+        if k != "outs" and v == tid:
+            return sizes[k]
+    raise KeyError(tid)
+
+
+@pytest.mark.parametrize("name", GRAPHS)
+def test_reference_graph_numerics_gate(G, orc, name):
+    print(f"reference graph {name}: numerics gate", flush=True)
+    ex, *_ = _executor(G, name, orc, num_streams=4, validate_numerics=True)
+    gate = ex.validate_numerics(repeats=5)
+    ex.close()
+    assert gate.passed, gate.detail
+    assert gate.configs_compared == 9, gate.detail

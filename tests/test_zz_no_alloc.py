@@ -93,3 +93,19 @@ def test_noalloc_rejections(gpu):
     assert int(m.launch_row_reduce_noalloc_f32(None, out, 1, 4, 0).code) == inval
     assert int(m.launch_row_reduce_noalloc_f32(x, out, 1, 4, 3).code) == inval
     assert m.launch_row_reduce_noalloc_f32(x, out, 0, 4, 0).ok()
+
+
+def test_noalloc_first_call_under_capture_replays_same_bits(gpu):
+    """The entry point's first call in a fresh process made under stream capture
+    (so its per-device scratch lookup runs while the stream captures), then the
+    graph replayed several times with eager calls on a smaller input in between:
+    every replay gives the workspace launch's bits (tests/noalloc_capture_child.py)."""
+    import os
+    import subprocess
+    import sys
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture_child.py")
+    p = subprocess.run([sys.executable, "-u", child], capture_output=True, text=True, timeout=110)
+    print(p.stdout)
+    print(p.stderr[-4000:])
+    assert p.returncode == 0, p.stdout + p.stderr[-4000:]
+    assert "NOALLOC_CAPTURE_OK" in p.stdout
