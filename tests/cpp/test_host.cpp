@@ -17,6 +17,7 @@
 #include <set>
 
 #include "check.hpp"
+#include "../../mini-cuda-kernel-engine_amd/csrc/fast_div.hpp"
 #include "mcke/graph/executor.hpp"
 #include "mcke/graph/graph.hpp"
 #include "mcke/graph/memory_plan.hpp"
@@ -923,6 +924,39 @@ TEST(first_bit_mismatch_helper) {
   CHECK_EQ(first_bit_mismatch(x, y, 16), std::size_t{16});
   y[2] = 7;
   CHECK_EQ(first_bit_mismatch(x, y, 16), std::size_t{8});
+}
+
+// The multiply-shift division the flat-grid bias+act kernel uses to split a
+// workgroup index into row and strip: equal to n / d for every divisor 1..4096
+// and the extreme divisors, at dividends around every multiple of d in range
+// and at the ends of [0, 2^31).
+TEST(fast_div_matches_division) {
+  std::vector<std::uint32_t> divisors;
+  for (std::uint32_t d = 1; d <= 4096; ++d) divisors.push_back(d);
+  for (std::uint32_t d : {6553u, 65535u, 65536u, 65537u, 1000003u, 16777215u, 16777216u,
+                          0x7FFFFFFEu, 0x7FFFFFFFu, 0x80000000u})
+    divisors.push_back(d);
+  std::mt19937 rng(12345);
+  int bad = 0;
+  for (std::uint32_t d : divisors) {
+    const mcke_amd::FastDivU32 f = mcke_amd::FastDivU32::make(d);
+    auto one = [&](std::uint64_t n) {
+      if (n >= 0x80000000ull) return;
+      const auto n32 = static_cast<std::uint32_t>(n);
+      if (f.div(n32) != n32 / d) ++bad;
+    };
+    for (std::uint64_t n = 0; n < 3000; ++n) one(n);
+    for (std::uint64_t n = 0x7FFFFFFFull; n > 0x7FFFFFFFull - 3000; --n) one(n);
+    // Around multiples of d spread over the range.
+    const std::uint64_t step = std::max<std::uint64_t>(d, (0x80000000ull / 2000) / d * d);
+    for (std::uint64_t q = step; q < 0x80000000ull; q += step) {
+      one(q - 1);
+      one(q);
+      one(q + 1);
+    }
+    for (int i = 0; i < 2000; ++i) one(rng() & 0x7FFFFFFFu);
+  }
+  CHECK(bad == 0);
 }
 
 int main(int argc, char** argv) { return check::run_all(argc, argv); }

@@ -106,6 +106,31 @@ def test_bias_act_row_streaming_path_and_starved_grid(gpu, orc):
         assert np.array_equal(golden_io.bits(got), golden_io.bits(y4)), (vw, mrb)
 
 
+@pytest.mark.parametrize("shape", [(4500, 1000), (50000, 12), (4097, 2052)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_bias_act_flat_grid_partial_strips(gpu, orc, shape):
+    """The flat-grid kernel (one workgroup per row strip, row and strip from a
+    multiply-shift division) where a row's last strip is partial (1000 and 2052
+    columns) or a row is narrower than one strip (12 columns): every width against
+    the oracle, and bit-equal to the capped 2-D grid that walks the rows."""
+    rows, cols = shape
+    x = orc.fill_normal(rows * cols, 0xF1A7 + cols, 0.0, 2.0)
+    b = orc.fill_random(cols, 0xF1A8, -0.5, 0.5)
+    for act in (0, 3):
+        want = orc.bias_act(x, b, rows, cols, act)
+        ref_bits = None
+        for vw, mrb in ((4, 0), (2, 0), (1, 0), (4, 9)):
+            got = run_bias_act(gpu, x, b, rows, cols, act, vw, max_row_blocks=mrb)
+            if act == 0:
+                assert np.array_equal(golden_io.bits(got), golden_io.bits(want)), (vw, mrb)
+            else:
+                r = orc.compare(got, want, 1e-6, 1e-6)
+                assert r.ok, f"vw={vw} mrb={mrb}: {r}"
+            if ref_bits is None:
+                ref_bits = golden_io.bits(got)
+            assert np.array_equal(golden_io.bits(got), ref_bits), (act, vw, mrb)
+
+
 def test_bias_act_width_invariance_and_starved_grid(gpu, orc):
     rows, cols = 300, 2048
     x = orc.fill_normal(rows * cols, 5)
@@ -141,13 +166,16 @@ def test_activation_special_values(gpu, orc, act):
 
 
 @pytest.mark.parametrize("act", [0, 1, 2, 3])
-def test_activation_unfused(gpu, orc, act):
-    n = 3 * 4096
+@pytest.mark.parametrize("n", [3 * 4096, 3 * 4096 + 20, 5])
+def test_activation_unfused(gpu, orc, act, n):
     x = orc.fill_normal(n, 11, 0.0, 3.0)
     want = orc.bias_act(x, np.zeros(n, np.float32), 1, n, act)
-    got = run_activation(gpu, x, n, act, 4)
-    r = orc.compare(got, want, 1e-6, 1e-6)
-    assert r.ok, str(r)
+    for vw in (4, 1):
+        if n % vw:
+            continue
+        got = run_activation(gpu, x, n, act, vw)
+        r = orc.compare(got, want, 1e-6, 1e-6)
+        assert r.ok, f"vw={vw}: {r}"
 
 
 def _sum_abs_floor(x2d):
