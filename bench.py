@@ -461,7 +461,7 @@ def measured_peaks(m, stream, gemm_ms, iters=5):
     return out
 
 
-def gemm_sweep(m, stream, warm_ms=150.0, timed_ms=40.0):
+def gemm_sweep(m, stream, warm_ms=150.0, timed_ms=40.0, sizes=(512, 1024, 2048, 4096, 8192)):
     """configs[0]'s sweep sizes (reported, not the headline), each beside the vendor
     library's sgemm (rocBLAS, the kCublasRef ceiling row) on the same buffers.
 
@@ -481,7 +481,7 @@ def gemm_sweep(m, stream, warm_ms=150.0, timed_ms=40.0):
         stream.synchronize()
         return e0.elapsed_ms(e1) / count
 
-    for n in (512, 1024, 2048, 4096, 8192):
+    for n in sizes:
         a = D.from_array(m.fill_random(n * n, 0x6E33A))
         b = D.from_array(m.fill_random(n * n, 0x8B10C))
         c = D.zeros(n * n)
@@ -1581,6 +1581,8 @@ def main(argv=None) -> int:
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-sweep", action="store_true", help="skip the GEMM size sweep")
+    p.add_argument("--sweep-sizes", default="512,1024,2048,4096,8192",
+                   help="square sizes of the GEMM sweep (with --only gemm_sweep it runs alone)")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="target CPU time of the GEMM slab's timed runs together")
     p.add_argument("--no-graph", action="store_true", help="skip the config-5 graph section")
@@ -1613,7 +1615,7 @@ def main(argv=None) -> int:
     stream = m.Stream()
     ops, keep, gemm_bufs = build_ops(m, stream, only)
 
-    if only is not None and not ops and not any(x.startswith("gemm_lp") for x in only):
+    if only is not None and not ops and not any(x.startswith(("gemm_lp", "gemm_sweep")) for x in only):
         print(f"bench.py: --only {args.only} names no op", file=sys.stderr)
         return 2
     log(f"warmup: {args.warmup} steps")
@@ -1646,7 +1648,9 @@ def main(argv=None) -> int:
             e = s["effective_resident"]
             log(f"{'':>20s} resident {e['avg_ms']:.4f} ms  {e['achieved']:.1f} GB/s effective")
 
-    sweep = [] if (args.no_sweep or only is not None) else gemm_sweep(m, stream)
+    run_sweep = not args.no_sweep and (only is None or any(x.startswith("gemm_sweep") for x in only))
+    sweep = gemm_sweep(m, stream, sizes=tuple(int(x) for x in args.sweep_sizes.split(",") if x)) \
+        if run_sweep else []
     lp_res, lp_verify = None, []
     if not args.no_lp and (only is None or any(x.startswith("gemm_lp") for x in only)):
         lp_res, lp_verify = gemm_lp_section(
