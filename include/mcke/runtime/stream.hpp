@@ -59,13 +59,6 @@ class Stream {
     MCKE_RETURN_IF_ERROR(detail::from_rc(mcke_rt_stream_create(&h), "Stream::create"));
     return Stream(static_cast<StreamHandle>(h), true);
   }
-  // A stream with a hardware queue of its own (mcke_rt_stream_create_dedicated):
-  // streams made this way never share a queue, so their work can overlap.
-  [[nodiscard]] static StatusOr<Stream> create_dedicated() {
-    void* h = nullptr;
-    MCKE_RETURN_IF_ERROR(detail::from_rc(mcke_rt_stream_create_dedicated(&h), "Stream::create_dedicated"));
-    return Stream(static_cast<StreamHandle>(h), true);
-  }
   Stream(const Stream&) = delete;
   Stream& operator=(const Stream&) = delete;
   Stream(Stream&& o) noexcept : handle_(o.handle_), owned_(o.owned_) { o.owned_ = false; }

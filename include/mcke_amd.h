@@ -229,15 +229,6 @@ int mcke_rt_device_synchronize(void);
 
 /* Streams are created non-blocking (stream.hpp:29-35) at default priority. */
 int mcke_rt_stream_create(void** out_stream);
-/* No reference counterpart: a stream with a hardware queue of its own.  HIP hands
- * ordinary streams out over a small shared pool of hardware queues
- * (GPU_MAX_HW_QUEUES), so two streams can share one queue and run one after the
- * other; a stream created with an explicit CU mask always gets a new queue.  The
- * mask given here holds every CU of the current device, so the stream may run on
- * all of them.  Such a stream synchronises with the legacy null stream (work
- * queued on stream 0 waits for it and it for stream 0).  The graph executor
- * creates the lanes of multi-stream plans this way. */
-int mcke_rt_stream_create_dedicated(void** out_stream);
 int mcke_rt_stream_destroy(void* stream);
 int mcke_rt_stream_synchronize(void* stream);
 /* *done = 1 when all work on the stream has completed. */

@@ -6,9 +6,7 @@
 //   query_device / set_device / raw_device_malloc/free device.cpp:56-130
 //   RawDeviceAllocator (one allocation per call)       allocator.cpp:44-73
 //   async H2D/D2H copies                               tensor.cpp:108-138
-// Streams are at default priority and non-blocking, except the dedicated-queue
-// streams (mcke_rt_stream_create_dedicated), which HIP creates with a CU mask and
-// which synchronise with the legacy null stream.
+// Streams are non-blocking and at default priority.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -122,21 +120,6 @@ int mcke_rt_stream_create(void** out_stream) {
   if (!out_stream) return invalid("mcke_rt_stream_create: null out");
   hipStream_t s = nullptr;
   MCKE_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
-  *out_stream = s;
-  return ok();
-}
-
-int mcke_rt_stream_create_dedicated(void** out_stream) {
-  if (!out_stream) return invalid("mcke_rt_stream_create_dedicated: null out");
-  int dev = 0, cus = 0;
-  MCKE_HIP_TRY(hipGetDevice(&dev));
-  MCKE_HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  if (cus <= 0) return fail(MCKE_STATUS_INTERNAL, "mcke_rt_stream_create_dedicated: no CUs reported");
-  // Bit i of word i / 32 enables CU i: every CU the device has.
-  std::vector<uint32_t> mask(static_cast<std::size_t>((cus + 31) / 32), 0xFFFFFFFFu);
-  if (cus % 32) mask.back() = (1u << (cus % 32)) - 1u;
-  hipStream_t s = nullptr;
-  MCKE_HIP_TRY(hipExtStreamCreateWithCUMask(&s, static_cast<uint32_t>(mask.size()), mask.data()));
   *out_stream = s;
   return ok();
 }

@@ -115,14 +115,9 @@ Status GraphExecutor::plan() {
   const std::size_t lanes = sa.num_streams_used;
   const std::size_t S = sa.nodes.size();
 
-  // Streams and events: cross-stream events, fork, joins.  The lanes of a
-  // multi-stream plan each get a hardware queue of their own: ordinary streams
-  // share HIP's small queue pool, and two lanes on one queue run one after the
-  // other (on gfx950, fanout4x4 with one queue shared took 0.45-0.48 ms against
-  // 0.31 ms with four).
+  // Streams and events: cross-stream events, fork, joins.
   for (std::size_t k = 0; k < lanes; ++k) {
-    MCKE_ASSIGN_OR_RETURN(rt::Stream lane,
-                          lanes > 1 ? rt::Stream::create_dedicated() : rt::Stream::create());
+    MCKE_ASSIGN_OR_RETURN(rt::Stream lane, rt::Stream::create());
     p.lanes_.push_back(std::move(lane));
   }
   const std::size_t n_signals = sa.num_events + (lanes > 1 ? lanes : 0);
