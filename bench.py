@@ -960,11 +960,13 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
         -> bias -> softmax, per-node times and roofline fractions;
       * a 4x4 fan-out of 2048^3 GEMM chains on 4 streams (chain-greedy and
         level-parallel) vs the same graph on one stream, with the overlap (sum of
-        node times / wall) and buddy statistics;
+        node medians / wall, both from a profiled run) and buddy statistics;
       * the reference graph bench's five graphs at its shapes (mcke_amd.graph.
         REFERENCE_GRAPHS: diamond of 2048^3 GEMMs, chain of 16 bias+GELU nodes,
         4x4 fan-out of starved bias+GELU chains, starved diamond, transformer
-        block), under the three schedules, with node sum / wall overlap;
+        block), under the three schedules, with the same overlap figure;
+      * every wall time from an executor without timing events between the nodes
+        (wall_ms), beside the profiled run's (wall_profiled_ms);
       * for every timed plan the launch-bound ratio (host enqueue time of one
         run / device time of one run, bench/graph_bench.cpp:437-441).
     Every one of these graphs also runs the numerics gate (3 schedules x 3 memory
@@ -1108,13 +1110,13 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
         wall_prof, _ = timed_runs(ex, steps)
         node_sum = sum(x["median_ms"] for x in ex.timings())
         fan[label] = {"wall_ms": round(wall, 4), "wall_profiled_ms": round(wall_prof, 4),
-                      "node_sum_ms": round(node_sum, 4), "overlap": round(node_sum / wall, 3),
+                      "node_sum_ms": round(node_sum, 4), "overlap": round(node_sum / wall_prof, 3),
                       "tflops": round(info["total_flops"] / (wall * 1e-3) / 1e12, 2),
                       "enqueue_us": round(enq, 2), "launch_bound_ratio": launch_bound(wall, enq),
                       "streams": info["num_streams_used"], "events": info["num_events"],
                       "waits": info["waits_dedup"], "arena_bytes": info["arena_bytes"],
                       "allocator": alloc_stats}
-        log(f"config 5 fan-out {label}: {wall:.3f} ms, overlap {node_sum / wall:.2f}")
+        log(f"config 5 fan-out {label}: {wall:.3f} ms, overlap {node_sum / wall_prof:.2f}")
         ex.close()
     for label in ("level_parallel_4streams", "chain_greedy_4streams"):
         fan[label]["speedup_vs_sequential"] = round(fan["sequential"]["wall_ms"] /
@@ -1171,7 +1173,7 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
             node_sum = sum(x["median_ms"] for x in ex.timings())
             rows[label] = {"wall_ms": round(wall, 4), "wall_profiled_ms": round(wall_prof, 4),
                            "node_sum_ms": round(node_sum, 4),
-                           "overlap": round(node_sum / wall, 3), "enqueue_us": round(enq, 2),
+                           "overlap": round(node_sum / wall_prof, 3), "enqueue_us": round(enq, 2),
                            "launch_bound_ratio": launch_bound(wall, enq),
                            "streams": info["num_streams_used"], "events": info["num_events"],
                            "waits": info["waits_dedup"],
