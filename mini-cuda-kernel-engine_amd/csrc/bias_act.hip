@@ -7,14 +7,15 @@
 //     issues 64 x VW x 4 contiguous bytes (1 KiB at VW = 4: a 16-byte
 //     global_load_dwordx4 per lane);
 //   * the bias vector for those columns is loaded once and kept in registers;
-//   * large launches: one workgroup per 1 KiB strip of a row (one wave at
-//     VW = 4) over a flat 1-D grid, so every lane has one vector load in flight,
-//     each wave's life is short (its row and strip come from a multiply-shift
+//   * large launches at VW = 4: one one-wave workgroup per 1 KiB strip of a row
+//     over a flat 1-D grid, so every lane has one 16-byte load in flight, each
+//     wave's life is short (its row and strip come from a multiply-shift
 //     division, no loop), and the hardware streams workgroups through the CUs in
 //     address order;
-//   * launches with a capped grid (max_row_blocks, the reference's starvation
-//     lever) or beyond the flat grid's 32-bit limits: a 2-D grid of column strips
-//     x row blocks that walks rows with a stride of gridDim.y, four per iteration;
+//   * narrower widths, launches with a capped grid (max_row_blocks, the
+//     reference's starvation lever) and tensors beyond the flat grid's 32-bit
+//     limits: a 2-D grid of column strips x row blocks that walks rows with a
+//     stride of gridDim.y, four per iteration (4 / VW rows per workgroup at once);
 //   * small launches (at most two rounds of resident workgroups at one row each):
 //     256-lane workgroups that each own kChunkRows adjacent rows of their column
 //     strip and issue all their loads before any store, so the launch is one
@@ -82,8 +83,8 @@ __global__ __launch_bounds__(NT) void bias_act_kernel(const float* __restrict__ 
   }
 }
 
-// Large launches: workgroup w of a flat grid owns strip (w mod strips) of row
-// (w / strips), NT lanes of VW columns each.  One load per lane, no loop: on gfx950
+// Large launches at VW = 4: workgroup w of a flat grid owns strip (w mod strips) of
+// row (w / strips), NT lanes of VW columns each.  One load per lane, no loop: on gfx950
 // this streamed 16384 x 4096 at 80.5 us against 83.0 us for the 2-D grid with its
 // row walk, and 16384 x 1024 (4 strips a row) at 21.3 us against 30 us, where the
 // 2-D grid dispatches poorly.
@@ -261,29 +262,34 @@ int launch_fused_vw(const float* x, const float* bias, float* y, int64_t rows, i
   }
   constexpr int L = kRowBytes / (4 * VW);
   // The flat grid: rows x strips workgroups of L lanes, within the 32-bit limits
-  // of the grid, of the global work size and of FastDivU32's operands.
-  const int64_t strips = (cols_v + L - 1) / L;
-  const int64_t flat = rows * strips;
-  if (max_row_blocks <= 0 && cols_v <= INT32_MAX && flat <= INT32_MAX &&
-      flat * L <= int64_t{UINT32_MAX}) {
-    const FastDivU32 by = FastDivU32::make(static_cast<uint32_t>(strips));
-    const dim3 g(static_cast<unsigned>(flat));
-    const uint32_t cv32 = static_cast<uint32_t>(cols_v), st32 = static_cast<uint32_t>(strips);
+  // of the grid, of the global work size and of FastDivU32's operands.  At VW = 4
+  // only: a lane then has a 16-byte load in flight, where at VW = 1 and 2 it would
+  // have 4 or 8 bytes (16384 x 4096: 153 us and 102 us, against 87 and 82 us for the
+  // 2-D grid, whose workgroups take 4 / VW rows at once).
+  if constexpr (VW == 4) {
+    const int64_t strips = (cols_v + L - 1) / L;
+    const int64_t flat = rows * strips;
+    if (max_row_blocks <= 0 && cols_v <= INT32_MAX && flat <= INT32_MAX &&
+        flat * L <= int64_t{UINT32_MAX}) {
+      const FastDivU32 by = FastDivU32::make(static_cast<uint32_t>(strips));
+      const dim3 g(static_cast<unsigned>(flat));
+      const uint32_t cv32 = static_cast<uint32_t>(cols_v), st32 = static_cast<uint32_t>(strips);
 #define MCKE_STRIP(A) bias_act_strip_kernel<VW, A, L><<<g, L, 0, s>>>(x, bias, y, cv32, st32, by)
-    switch (act) {
-      case kActNone: MCKE_STRIP(kActNone); break;
-      case kActRelu: MCKE_STRIP(kActRelu); break;
-      case kActGeluErf: MCKE_STRIP(kActGeluErf); break;
-      case kActGeluTanh: MCKE_STRIP(kActGeluTanh); break;
-      default: return invalid("launch_bias_act_f32: unknown activation " + std::to_string(act));
-    }
+      switch (act) {
+        case kActNone: MCKE_STRIP(kActNone); break;
+        case kActRelu: MCKE_STRIP(kActRelu); break;
+        case kActGeluErf: MCKE_STRIP(kActGeluErf); break;
+        case kActGeluTanh: MCKE_STRIP(kActGeluTanh); break;
+        default: return invalid("launch_bias_act_f32: unknown activation " + std::to_string(act));
+      }
 #undef MCKE_STRIP
-    MCKE_LAUNCH_CHECK("bias_act_strip_kernel");
-    return ok();
+      MCKE_LAUNCH_CHECK("bias_act_strip_kernel");
+      return ok();
+    }
   }
-  // Capped or very large grids.  Below VW = 4 each workgroup takes 4 / VW rows at
-  // once (the kernel's unrolled row walk), so a lane still has 16 bytes of loads
-  // in flight.
+  // Narrower widths, capped grids and very large tensors: the 2-D grid.  Below
+  // VW = 4 each workgroup takes 4 / VW rows at once (the kernel's unrolled row
+  // walk), so a lane still has 16 bytes of loads in flight.
   const dim3 grid = grid_2d(rows, cols_v, max_row_blocks, L, 4 / VW);
   switch (act) {
     case kActNone: bias_act_kernel<VW, kActNone, L><<<grid, L, 0, s>>>(x, bias, y, rows, cols_v); break;

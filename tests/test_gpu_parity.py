@@ -109,10 +109,11 @@ def test_bias_act_row_streaming_path_and_starved_grid(gpu, orc):
 @pytest.mark.parametrize("shape", [(4500, 1000), (50000, 12), (4097, 2052)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_bias_act_flat_grid_partial_strips(gpu, orc, shape):
-    """The flat-grid kernel (one workgroup per row strip, row and strip from a
-    multiply-shift division) where a row's last strip is partial (1000 and 2052
-    columns) or a row is narrower than one strip (12 columns): every width against
-    the oracle, and bit-equal to the capped 2-D grid that walks the rows."""
+    """The flat-grid kernel of VW = 4 (one workgroup per row strip, row and strip
+    from a multiply-shift division) where a row's last strip is partial (1000 and
+    2052 columns) or a row is narrower than one strip (12 columns), against the
+    oracle and bit-equal to the 2-D grid that walks the rows (VW = 2 and 1, and
+    VW = 4 with a capped grid)."""
     rows, cols = shape
     x = orc.fill_normal(rows * cols, 0xF1A7 + cols, 0.0, 2.0)
     b = orc.fill_random(cols, 0xF1A8, -0.5, 0.5)
