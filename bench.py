@@ -1518,8 +1518,8 @@ def headline(detail: dict, detail_file: str | None) -> dict:
     GEMM's roofline, the CPU baseline's summary and one short row per op, in the
     spirit of the reference's one-CSV-row-per-kernel profiler record
     (src/core/profiler.cpp:95-113).  Every other section stays in `detail`, which
-    bench.py writes to `detail_file`.  Kept under HEADLINE_MAX_BYTES: extra keys
-    are dropped, least important first, until it fits."""
+    bench.py writes to `detail_file`.  Kept under HEADLINE_MAX_BYTES: the section
+    summaries are dropped, least important first, until it fits."""
     keep = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
             "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config", "roofline")
     line = {k: detail.get(k) for k in keep}
@@ -1564,12 +1564,27 @@ def headline(detail: dict, detail_file: str | None) -> dict:
         extra["graph_capture_choice"] = {
             k: [v["eager_us_per_run"], v["replay_us_per_run"], v["captured"]]
             for k, v in graph["capture_choice"].items()}
-    parity = [s.get("parity", {}).get("ok") for s in detail.get("ops") or [] if s.get("parity")]
-    extra["all_parity_ok"] = all(parity) if parity else None
+    # Every parity verdict in the record (ops, 16-bit GEMM, graphs, ladder, CPU legs).
+    verdicts = []
+
+    def walk(node):
+        if isinstance(node, dict):
+            p = node.get("parity")
+            if isinstance(p, dict) and isinstance(p.get("ok"), bool):
+                verdicts.append(p["ok"])
+            for v in node.values():
+                walk(v)
+        elif isinstance(node, list):
+            for v in node:
+                walk(v)
+    walk(detail)
+    extra["all_parity_ok"] = all(verdicts) if verdicts else None
+    extra["parity_checks"] = len(verdicts)
     extra["detail_file"] = detail_file
     line.update(extra)
+    # Only the summaries may go; the contract fields always stay.
     for k in ("graph_capture_choice", "graph_mlp", "gemm_lp_tflops", "gemm_sweep_tflops",
-              "measured_peaks", "data"):
+              "measured_peaks"):
         if len(json.dumps(line, separators=(",", ":"))) <= HEADLINE_MAX_BYTES:
             break
         line.pop(k, None)

@@ -141,7 +141,12 @@ def test_headline_is_compact_and_carries_the_contract():
     for row in line["ops"]:
         assert len(row) == len(line["ops_columns"]) and row[5] is True
     assert line["all_parity_ok"] is True
+    assert line["parity_checks"] == len(ALGORITHMIC)
     assert line["detail_file"] == "gpurun_out/bench_detail.json"
+    # One failed check anywhere in the record shows in the headline.
+    detail["graph"]["reference_graphs"] = {"fanout4x4": {"parity": {"ok": False}}}
+    bad = bench.headline(detail, None)
+    assert bad["all_parity_ok"] is False and bad["parity_checks"] == len(ALGORITHMIC) + 1
     assert json.loads(text) == line
 
 
