@@ -338,7 +338,10 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_lp_kernel(
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < NT; ++j) acc[i][j] = MF::run(av[i], bv[j], acc[i][j]);
+        for (int jj = 0; jj < NT; ++jj) {
+          const int j = mfma_snake_col(i, jj, NT);
+          acc[i][j] = MF::run(av[i], bv[j], acc[i][j]);
+        }
       __builtin_amdgcn_sched_barrier(0);
       // ...and their LDS stores (into the buffer nobody reads this step) over 2-3.
       if (s == 2) {
@@ -517,7 +520,7 @@ __device__ __forceinline__ void lp_dma_slot(f32x16 (&acc)[BM / 64][BN / 64],
                                             const uint32_t (&b_src)[LpDmaShape<BM, BN, STAGES>::NB],
                                             int kstep, uint32_t dstage, uint32_t wave) {
   using S = LpDmaShape<BM, BN, STAGES>;
-  constexpr int i = IDX / S::NT, j = IDX % S::NT;
+  constexpr int i = IDX / S::NT, j = mfma_snake_col(i, IDX % S::NT, S::NT);
   const u32x4 b = u32x4{cbv[j][0][0], cbv[j][0][1], cbv[j][1][0], cbv[j][1][1]};
   // TRANS: operands swapped, the MFMA computes the transposed tile (n rows, m columns).
   if constexpr (TRANS) acc[i][j] = LpMfma<T>::run(b, cav[i], acc[i][j]);
@@ -992,8 +995,9 @@ __device__ __forceinline__ void lp16_slot(f32x4 (&acc)[BM / 32][BN / 32],
                                           uint32_t wave) {
   using S = Lp16Shape<BM, BN>;
   constexpr int NT = S::NT;
-  constexpr int i = IDX / NT, j = IDX % NT;
-  if constexpr (j == 0) {
+  // jj: position within block row i; j: the column it computes (mfma_snake_col).
+  constexpr int i = IDX / NT, jj = IDX % NT, j = mfma_snake_col(i, jj, NT);
+  if constexpr (jj == 0) {
     lds_wait_n<S::wait_before_row(i)>();
     touch_a<i, i + 1>(av[P]);
     if constexpr (i == 0) touch_b<0, NT>(bv[P]);

@@ -45,6 +45,19 @@ constexpr int kMfmaThreads = 256;
 constexpr int kXcds = 8;       // gfx950: workgroups are dealt round-robin to 8 XCDs
 constexpr int kGroupM = 8;     // tile-row grouping for L2 reuse within an XCD
 
+// MFMA order within a step.  Block row i of a wave's MT x NT accumulators walks
+// its columns left to right when i is even and right to left when i is odd, so
+// each MFMA shares one operand register with the one before it: the A fragment
+// along a row, the B fragment at a row turn.  With random operands the matrix
+// pipe runs at the board's power limit, where fewer operand bits changing from
+// one MFMA to the next buy engine clock (measured on MI355X, same process,
+// alternating blocks: 16-bit GEMM 8192^3 +0.8%, 4096^3 +0.7%; fp32 8192^3 +0.3%,
+// 2048^3 +1.7%).  Every accumulator still takes its K sub-steps in the same
+// order, so the results are bit-identical to row order.
+__host__ __device__ constexpr int mfma_snake_col(int i, int jj, int nt) {
+  return (i % 2) ? nt - 1 - jj : jj;
+}
+
 template <int NT> struct BVec;
 template <> struct BVec<1> { using type = float; };
 template <> struct BVec<2> { using type = f32x2; };
@@ -454,7 +467,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
 #pragma unroll
-          for (int j = 0; j < NT; ++j) {
+          for (int jj = 0; jj < NT; ++jj) {
+            const int j = mfma_snake_col(i, jj, NT);
             float bj;
             if constexpr (NT == 1) bj = bv; else bj = bv[j];
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], bj, acc[i][j], 0, 0, 0);
@@ -742,7 +756,8 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
 #pragma unroll
           for (int i = 0; i < MT; ++i) {
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
+            for (int jj = 0; jj < NT; ++jj) {
+              const int j = mfma_snake_col(i, jj, NT);
               float bj;
               if constexpr (NT == 1) bj = bf[PP][p]; else bj = bf[PP][p][j];
               acc[i][j] =
@@ -822,7 +837,8 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
 #pragma unroll
           for (int i = 0; i < MT; ++i) {
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
+            for (int jj = 0; jj < NT; ++jj) {
+              const int j = mfma_snake_col(i, jj, NT);
               float bj;
               if constexpr (NT == 1) bj = bv; else bj = bv[j];
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], bj, acc[i][j], 0, 0, 0);
@@ -889,7 +905,8 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
   #pragma unroll
           for (int i = 0; i < MT; ++i) {
   #pragma unroll
-            for (int j = 0; j < NT; ++j) {
+            for (int jj = 0; jj < NT; ++jj) {
+              const int j = mfma_snake_col(i, jj, NT);
               float bj;
               if constexpr (NT == 1) bj = bv; else bj = bv[j];
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], bj, acc[i][j], 0, 0, 0);
