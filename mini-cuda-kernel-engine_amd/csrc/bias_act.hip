@@ -363,6 +363,10 @@ int mcke_launch_bias_act_f32(const float* x, const float* bias, float* y, int64_
     return invalid("launch_bias_act_f32: in-place (x == y) violates the __restrict__ contract");
   if (act < 0 || act > 3)
     return invalid("launch_bias_act_f32: unknown activation " + std::to_string(act));
+  // Column strips x their lanes (at most 1024 a strip) must fit the grid's 32-bit
+  // global work size along x.
+  if (cols / vector_width > int64_t{UINT32_MAX} - 1023)
+    return invalid("launch_bias_act_f32: cols / vector_width exceeds the grid's 32-bit work size");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (vector_width) {
     case 1: return launch_fused_vw<1>(x, bias, y, rows, cols, act, s, max_row_blocks);

@@ -175,7 +175,8 @@ def _no_gpu(mcke) -> bool:
 @pytest.fixture()
 def cpu_only(mcke):
     if not _no_gpu(mcke):
-        pytest.skip("a GPU is visible: tests/test_gpu_errors.py covers this with real buffers")
+        pytest.skip("a GPU is visible: these calls pass fake device addresses, so they run only "
+                    "where a missed rejection cannot launch a kernel on them")
     return mcke
 
 
@@ -208,6 +209,8 @@ def test_bias_act_rejections(cpu_only):
     assert m.launch_bias_act_f32(X, B, X, 4, 8, 3, 4).code == IA              # in place
     assert m.launch_bias_act_f32(X, B, Y, 4, 8, 9, 4).code == IA              # bad act
     assert m.launch_activation_f32(X, Y, 6, 3, 4).code == IA                  # n % vw
+    st = m.launch_bias_act_f32(X, B, Y, 1, 1 << 33, 3, 1)                    # grid x > 2^32 lanes
+    assert st.code == IA and "32-bit work size" in st.message
 
 
 def test_reduce_rejections(cpu_only):
