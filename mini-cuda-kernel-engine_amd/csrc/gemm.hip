@@ -450,6 +450,9 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
                                          static_cast<int64_t>(32) * n < (int64_t{1} << 30)));
     MfmaFn fn = whole ? sp.mfma_even : sp.mfma;
     const dim3 block = whole ? dim3(static_cast<unsigned>(sp.even_threads), 1, 1) : sp.block;
+    if (tiles_m * tiles_n * static_cast<int64_t>(block.x) > int64_t{UINT32_MAX})
+      return invalid("launch_gemm_f32: tiles x lanes exceed the grid's 32-bit work size; use a "
+                     "larger tile");
     fn<<<static_cast<unsigned>(tiles_m * tiles_n), block, 0, s>>>(
         a, b, c, mi, ni, ki, alpha, beta, static_cast<int>(tiles_m), static_cast<int>(tiles_n));
     MCKE_LAUNCH_CHECK("gemm_mfma_kernel");
@@ -461,7 +464,8 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
   const int64_t gx = (n + sp.tile_n - 1) / sp.tile_n;
   const int64_t gy = (m + sp.tile_m - 1) / sp.tile_m;
   if (gy > 65535) return invalid("launch_gemm_f32: m too large for the grid's y limit");
-  if (gx > 2147483647LL) return invalid("launch_gemm_f32: n too large for the grid");
+  if (gx * static_cast<int64_t>(sp.block.x) > int64_t{UINT32_MAX})
+    return invalid("launch_gemm_f32: n too large for the grid's 32-bit work size");
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), 1);
   sp.fn<<<grid, sp.block, 0, s>>>(a, b, c, mi, ni, ki, alpha, beta);
   MCKE_LAUNCH_CHECK("gemm kernel");

@@ -41,8 +41,9 @@ struct LpTile {
                     float beta, bool vec, hipStream_t s) {
     const int64_t tiles_m = (static_cast<int64_t>(m) + BM - 1) / BM;
     const int64_t tiles_n = (static_cast<int64_t>(n) + BN - 1) / BN;
-    if (tiles_m * tiles_n > 2147483647LL)
-      return invalid("launch_gemm_lp: too many tiles for one launch");
+    if (tiles_m * tiles_n * kMfmaThreads > int64_t{UINT32_MAX})
+      return invalid("launch_gemm_lp: tiles x lanes exceed the grid's 32-bit work size; use a "
+                     "larger tile");
     const bool even = vec && m % BM == 0 && n % BN == 0 && k % kLpBK == 0;
     const auto* A = static_cast<const uint16_t*>(a);
     const auto* B = static_cast<const uint16_t*>(b);

@@ -257,6 +257,12 @@ def test_gemm_rejections(cpu_only):
     assert m.launch_gemm_f32(X, B, Y, 8, 8, 8, 1, 0, 42, good).code == IA
     # the ladder's 2-D grid caps the row tiles at 65535
     assert m.launch_gemm_f32(X, B, Y, 65536 * 4 + 1, 8, 8, 1, 0, V.kNaive, T()).code == IA
+    # tiles x lanes beyond the grid's 32-bit work size: 4096^2 32 x 32 tiles of 256 lanes,
+    # and 2^26 column tiles of 64 lanes for the uncoalesced ladder kernel
+    st = m.launch_gemm_f32(X, B, Y, 1 << 17, 1 << 17, 8, 1, 0, V.kMfmaF32, T(32, 32, 32, 2, 2))
+    assert st.code == IA and "32-bit work size" in st.message
+    st = m.launch_gemm_f32(X, B, Y, 8, 1 << 28, 8, 1, 0, V.kNaiveUncoalesced, T())
+    assert st.code == IA and "32-bit work size" in st.message
 
 
 def test_default_lp_tile(mcke):
@@ -287,3 +293,5 @@ def test_gemm_lp_rejections(cpu_only):
     assert st.code == IA and "no fallback" in st.message
     st, _ = m.gemm_lp_kernel_attrs(f16, f32, T(128, 128, 8, 8, 8))
     assert st.code == IA
+    st = m.launch_gemm_lp(X, B, Y, bf, f32, 1 << 18, 1 << 18, 64, 1, 0, T(64, 64, 64, 4, 4))
+    assert st.code == IA and "32-bit work size" in st.message                       # 2^24 tiles
