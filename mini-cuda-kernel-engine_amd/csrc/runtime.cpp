@@ -398,6 +398,7 @@ int mcke_rt_memset_async(void* dst, int value, size_t bytes, void* stream) {
 
 // ---- host data generators --------------------------------------------------
 void mcke_fill_random_f32(float* host, size_t n, uint64_t seed, float lo, float hi) {
+  if (!host) return;
   std::mt19937_64 eng(seed);
   const float span = hi - lo;
   for (size_t i = 0; i < n; ++i) {
@@ -407,6 +408,7 @@ void mcke_fill_random_f32(float* host, size_t n, uint64_t seed, float lo, float 
 }
 
 void mcke_fill_normal_f32(float* host, size_t n, uint64_t seed, float mu, float sigma) {
+  if (!host) return;
   std::mt19937_64 eng(seed);
   const double two_pi = 6.283185307179586476925286766559;
   const double inv53 = 1.0 / 9007199254740992.0;
