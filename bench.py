@@ -1626,9 +1626,18 @@ def main(argv=None) -> int:
         print("bench.py: need --steps >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
 
+    # The graph section's multi-stream plans want a hardware queue per executor lane.
+    # HIP hands streams out over GPU_MAX_HW_QUEUES queues per process (4 by default)
+    # and, once each holds a stream, puts a new stream on a queue it shares, so two
+    # lanes of a plan created after the bench's other streams can run one after the
+    # other (fanout4x4 under chain-greedy: 1.48x over one stream with 4 queues, 2.13-2.17x
+    # with 8 or 16, measured on MI355X).  Read when HIP initialises, i.e. before the
+    # library loads; a value the caller exported wins.
+    os.environ.setdefault("GPU_MAX_HW_QUEUES", "8")
     m = load_package()
     info = m.require_gpu()
-    log(f"device: {info.name.decode()} {info.arch.decode()} CUs={info.sm_count}")
+    log(f"device: {info.name.decode()} {info.arch.decode()} CUs={info.sm_count} "
+        f"hw_queues={os.environ['GPU_MAX_HW_QUEUES']}")
     stream = m.Stream()
     ops, keep, gemm_bufs = build_ops(m, stream, only)
 
@@ -1732,6 +1741,7 @@ def main(argv=None) -> int:
             "gemm_tile": list(m.gemm_mfma_default_tile(8192, 8192, 8192).astuple()),
             # The runtime leaves the marketing name empty on some boxes.
             "device": info.name.decode() or f"{info.arch.decode()} ({info.sm_count} CUs)",
+            "hw_queues": os.environ.get("GPU_MAX_HW_QUEUES"),
         },
         "roofline": {
             "bound": gemm["bound"], "achieved": gemm["achieved"], "peak": gemm["peak"],
