@@ -1631,9 +1631,10 @@ def main(argv=None) -> int:
     # and, once each holds a stream, puts a new stream on a queue it shares, so two
     # lanes of a plan created after the bench's other streams can run one after the
     # other (fanout4x4 under chain-greedy: 1.48x over one stream with 4 queues, 2.13-2.17x
-    # with 8 or 16, measured on MI355X).  Read when HIP initialises, i.e. before the
-    # library loads; a value the caller exported wins.
-    os.environ.setdefault("GPU_MAX_HW_QUEUES", "8")
+    # with 8 or 16, measured on MI355X).  HIP reads it when it initialises, i.e. before
+    # the library loads.  The bench runs with 8 (MCKE_BENCH_HW_QUEUES picks another
+    # value) and records it in config.hw_queues.
+    os.environ["GPU_MAX_HW_QUEUES"] = os.environ.get("MCKE_BENCH_HW_QUEUES", "8")
     m = load_package()
     info = m.require_gpu()
     log(f"device: {info.name.decode()} {info.arch.decode()} CUs={info.sm_count} "
