@@ -206,6 +206,42 @@ def test_row_reduce_random(gpu, orc, variant, shape):
             assert r.ok, f"kind={kind}: {r}"
 
 
+@pytest.mark.parametrize("cols", [5, 1000, 70000])
+def test_row_reduce_special_values(gpu, orc, cols):
+    """Sum, max and mean of rows holding +inf, -inf, both, NaN, or huge values, every
+    variant: the same NaN / +-inf pattern as the double-precision reference
+    (reference.hpp:154-172), finite results at its bar.  A row with +inf and -inf sums
+    to NaN in any order; max skips NaN as fmaxf does (the reference kernel's MaxOp,
+    reduce_ops.cuh:38-119) and as the reference's std::max(m, v) from -inf does, so
+    an all-NaN row has max -inf."""
+    rng = np.random.default_rng(cols)
+    x = rng.normal(0.0, 1.0, (7, cols)).astype(np.float32)
+    x[0, cols // 2] = np.inf
+    x[1, 0] = -np.inf
+    x[2, 1 % cols] = np.inf
+    x[2, cols - 1] = -np.inf
+    x[3, cols // 3] = np.nan
+    x[4, 0] = 3e38                                # huge but finite: the double sum stays finite
+    x[6, :] = np.nan                              # row 5 stays finite
+    x = x.ravel()
+    assert orc.row_reduce(x, 7, cols, 1)[6] == -np.inf
+    for kind in (0, 1, 2):
+        want = orc.row_reduce(x, 7, cols, kind)
+        for variant in (0, 1, 2):
+            got = run_reduce(gpu, x, 7, cols, kind, variant)
+            params = f"kind={kind} variant={variant}"
+            assert np.array_equal(np.isnan(got), np.isnan(want)), (params, got, want)
+            inf_w = np.isinf(want)
+            assert np.array_equal(got[inf_w], want[inf_w]), (params, got, want)
+            fin = np.isfinite(want)
+            if kind == 1:
+                assert np.array_equal(got[fin], want[fin]), params
+            else:
+                floor = _sum_abs_floor(x.reshape(7, cols)[5:6]) / (cols if kind == 2 else 1)
+                r = orc.compare(got[fin], want[fin], 1e-5, floor)
+                assert r.ok, f"{params}: {r}"
+
+
 def test_row_reduce_all_negative_and_inf_rows(gpu, orc):
     x = np.array([[-5, -1, -9, -3], [-np.inf] * 4, [1, np.nan, 3, 2]], np.float32)
     for variant in (0, 1, 2):
@@ -226,6 +262,52 @@ def test_softmax_random(gpu, orc, variant, cols):
     assert r.ok, str(r)
     sums = got.reshape(rows, cols).astype(np.float64).sum(axis=1)
     assert np.max(np.abs(sums - 1.0)) <= 1e-5
+
+
+@pytest.mark.parametrize("cols", [7, 8, 1024, 1031, 8200])
+def test_softmax_special_values(gpu, orc, cols):
+    """Rows with infinities, NaN, huge and tiny magnitudes against the double-precision
+    reference (reference.hpp:175-191): its max keeps the running value against NaN
+    (std::max(m, v)), so a NaN entry, a +inf entry or a row of -inf makes the whole
+    row NaN through the sum, while -inf and -FLT_MAX entries beside finite ones get 0.
+    Every kernel path: cols 7 and 1031 take the element path, 8 and 1024 the
+    register-resident kernel, 8200 the one-pass online kernel on 16-byte data; both
+    variants.  NaN positions must match; other entries rel 1e-5 + abs 1e-6."""
+    fmax = np.finfo(np.float32).max
+    rng = np.random.default_rng(cols)
+    rows = []
+
+    def row(specials):
+        r = rng.normal(0.0, 2.0, cols).astype(np.float32)
+        for j, v in specials.items():
+            r[j % cols] = v
+        rows.append(r)
+
+    row({1: -np.inf})                                            # -inf beside finite values
+    rows.append(np.full(cols, -np.inf, np.float32))              # all -inf: NaN
+    row({cols // 2: np.nan})                                     # NaN: NaN row
+    row({cols - 1: np.inf})                                      # +inf: NaN row
+    row({0: 3e38, 2: -3e38, 3: 1e38})                            # huge: differences overflow to -inf
+    row({0: 1e-30, 1: -1e-30, 2: 0.0, 3: -0.0})                  # tiny and signed zeros
+    row({0: -fmax, 3: -fmax})                                    # -FLT_MAX beside finite values
+    r = np.full(cols, -np.inf, np.float32)
+    r[cols // 3] = -fmax                                         # one -FLT_MAX among -inf: 1 there
+    rows.append(r)
+    x = np.concatenate(rows)
+    n_rows = len(rows)
+    want = orc.row_softmax(x, n_rows, cols)
+    nan_w = np.isnan(want)
+    # The cases above pin the reference's semantics, not just this oracle's.
+    assert nan_w.reshape(n_rows, cols).all(axis=1).tolist() == [False, True, True, True, False,
+                                                                False, False, False]
+    assert want[7 * cols + cols // 3] == 1.0
+    for variant in (0, 1):
+        got = run_softmax(gpu, x, n_rows, cols, variant)
+        nan_g = np.isnan(got)
+        assert np.array_equal(nan_w, nan_g), \
+            f"variant {variant}: NaN rows {np.nonzero(nan_w != nan_g)[0] // cols}"
+        r = orc.compare(got[~nan_w], want[~nan_w], 1e-5, 1e-6)
+        assert r.ok, f"variant {variant}: {r}"
 
 
 def test_softmax_overflow_ramp(gpu, orc):
@@ -253,6 +335,41 @@ def test_gemm_random(gpu, orc, shape):
     for cfg in gemm_configs(gpu):
         got = run_gemm(gpu, a, b, c, M, N, K, 1.0, 0.0, *cfg)
         r = orc.compare(got, want, rel, floor)
+        assert r.ok, f"{cfg_id(cfg)}: {r}"
+
+
+@pytest.mark.parametrize("shape", [(67, 45, 39), (256, 256, 64)], ids=lambda s: "x".join(map(str, s)))
+def test_gemm_special_values(gpu, orc, shape):
+    """Infinities and NaN in A and B, through every variant and tile: C holds NaN and
+    +-inf exactly where the double-precision reference (reference.hpp:199-211) does,
+    which no summation order changes (x + inf = inf for finite x, inf - inf = NaN,
+    0 * inf = NaN); finite entries at the K-scaled bar.  Rows of A and columns of B
+    each get one kind of special value, so every output pattern occurs: a single
+    +inf or -inf, both signs in one dot product, a NaN, and inf times an exact zero."""
+    M, N, K = shape
+    rng = np.random.default_rng(M * N + K)
+    a = rng.uniform(-1.0, 1.0, (M, K)).astype(np.float32)
+    b = rng.uniform(-1.0, 1.0, (K, N)).astype(np.float32)
+    a[0, 3] = np.inf                        # row 0: +inf times B row 3
+    a[1, 5] = -np.inf                       # row 1: -inf times B row 5
+    a[2, 1], a[2, 2] = np.inf, -np.inf      # row 2: both signs in one dot product
+    a[3, K - 1] = np.nan                    # row 3: NaN
+    a[4, 7] = np.inf                        # row 4: +inf times B row 7, which is
+    b[7, : N // 2] = 0.0                    #   zero over half the columns (0 * inf)
+    b[K - 2, N - 1] = np.inf                # column N-1: +inf down B
+    b[9, N - 2] = np.nan                    # column N-2: NaN
+    c = np.zeros(M * N, np.float32)
+    want = orc.gemm(a.ravel(), b.ravel(), c, M, N, K, 1.0, 0.0)
+    nan_w, inf_w = np.isnan(want), np.isinf(want)
+    assert nan_w.any() and inf_w.any() and (~nan_w & ~inf_w).any()
+    fin = ~nan_w & ~inf_w
+    amax = 1.0
+    for cfg in gemm_configs(gpu):
+        got = run_gemm(gpu, a.ravel(), b.ravel(), c, M, N, K, 1.0, 0.0, *cfg)
+        assert np.array_equal(np.isnan(got), nan_w), \
+            f"{cfg_id(cfg)}: NaN at {np.argwhere((np.isnan(got) != nan_w).reshape(M, N))[:5]}"
+        assert np.array_equal(got[inf_w], want[inf_w]), cfg_id(cfg)
+        r = orc.compare(got[fin], want[fin], orc.tol_gemm(K), orc.abs_tol_gemm(K, amax))
         assert r.ok, f"{cfg_id(cfg)}: {r}"
 
 

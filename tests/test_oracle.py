@@ -323,6 +323,31 @@ def test_ref_softmax_bit_equal(orc):
 
 
 @needs_ref
+def test_ref_softmax_special_values_bit_equal(orc):
+    """Rows with -inf, NaN, +inf, +-3e38, tiny values and -FLT_MAX: the restatement
+    keeps the reference's NaN handling in the max (std::max(m, v) keeps m) bit for bit,
+    including which rows come out NaN."""
+    fmax = np.finfo(np.float32).max
+    cols = 37
+    base = orc.fill_normal(8 * cols, 5, 0.0, 2.0).reshape(8, cols)
+    base[0, 1] = -np.inf
+    base[1, :] = -np.inf
+    base[2, 9] = np.nan
+    base[3, 36] = np.inf
+    base[4, :3] = (3e38, -3e38, 1e38)
+    base[5, :4] = (1e-30, -1e-30, 0.0, -0.0)
+    base[6, (0, 3)] = -fmax
+    base[7, :] = -np.inf
+    base[7, 12] = -fmax
+    x = base.ravel()
+    got = orc.row_softmax(x, 8, cols)
+    assert np.array_equal(golden_io.bits(orc.Ref.row_softmax(x, 8, cols)), golden_io.bits(got))
+    assert np.isnan(got.reshape(8, cols)).all(axis=1).tolist() == [False, True, True, True,
+                                                                   False, False, False, False]
+    assert got[7 * cols + 12] == 1.0
+
+
+@needs_ref
 def test_ref_gemm_bit_equal(orc):
     m, n, k = 29, 31, 37
     a = orc.fill_random(m * k, 0x6E33A)
