@@ -141,6 +141,44 @@ def test_unaligned_and_ragged_take_the_element_path_with_same_bits(gpu, orc, dt)
 
 @pytest.mark.parametrize("dt", DTS, ids=DT_ID.get)
 @pytest.mark.parametrize("out", ["f32", "same"])
+@pytest.mark.parametrize("shape", [(67, 45, 39), (256, 256, 64)], ids=lambda s: "x".join(map(str, s)))
+def test_special_values(gpu, orc, dt, out, shape):
+    """16-bit infinities and NaN in A and B, every tile, ragged (element path) and
+    whole-tile (direct-to-LDS kernel) shapes: NaN and +-inf in C exactly where the
+    oracle has them (no summation order changes those), finite entries within
+    tol_gemm(k) plus one output ulp for 16-bit C."""
+    M, N, K = shape
+    cd = F32 if out == "f32" else dt
+    rng = np.random.default_rng(M + N + K)
+    a = rng.uniform(-1.0, 1.0, (M, K)).astype(np.float32)
+    b = rng.uniform(-1.0, 1.0, (K, N)).astype(np.float32)
+    a[0, 3] = np.inf
+    a[1, 5] = -np.inf
+    a[2, 1], a[2, 2] = np.inf, -np.inf
+    a[3, K - 1] = np.nan
+    a[4, 7] = np.inf
+    b[7, : N // 2] = 0.0
+    b[K - 2, N - 1] = np.inf
+    b[9, N - 2] = np.nan
+    a16, b16 = orc.to_16(a, dt), orc.to_16(b, dt)
+    c = np.zeros(M * N, np.float32) if cd == F32 else np.zeros(M * N, np.uint16)
+    want = orc.gemm_lp(a16, b16, c, M, N, K, 1.0, 0.0, dt, cd)
+    w = want if cd == F32 else orc.from_16(want, dt)
+    nan_w, inf_w = np.isnan(w), np.isinf(w)
+    assert nan_w.any() and inf_w.any()
+    fin = ~nan_w & ~inf_w
+    rel = orc.tol_gemm(K) + (0.0 if cd == F32 else OUT_ULP[dt])
+    for tile in (gpu.gemm_lp_default_tile(M, N, K),) + tuple(gpu.LP_TILES):
+        got = run_lp(gpu, a16, b16, c, M, N, K, 1.0, 0.0, dt, cd, tile)
+        g = got if cd == F32 else orc.from_16(got, dt)
+        assert np.array_equal(np.isnan(g), nan_w), tile
+        assert np.array_equal(g[inf_w], w[inf_w]), tile
+        r = orc.compare(g[fin], w[fin], rel, orc.abs_tol_gemm(K))
+        assert r.ok, f"{tile}: {r}"
+
+
+@pytest.mark.parametrize("dt", DTS, ids=DT_ID.get)
+@pytest.mark.parametrize("out", ["f32", "same"])
 def test_beta_zero_does_not_read_c_and_k_zero_scales_c(gpu, orc, dt, out):
     M, N, K = 96, 80, 64
     cd = F32 if out == "f32" else dt
