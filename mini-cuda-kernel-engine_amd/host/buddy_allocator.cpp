@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <bit>
 #include <sstream>
+#include <string>
 
 #include "mcke/core/device.hpp"
 
@@ -234,10 +235,25 @@ Status BuddyAllocator::deallocate(const Allocation& a, rt::StreamHandle stream) 
     bypassed_.erase(b);
     return OkStatus();
   }
+  // Error codes as the reference's (buddy_allocator.cpp:557-576): a handle that
+  // names no live block of this allocator is an invalid argument, a block of one
+  // of its slabs that is not live (a double free) a failed precondition.
   auto it = live_.find(a.ptr);
-  if (it == live_.end())
-    return InvalidArgumentError("BuddyAllocator::deallocate: pointer was not allocated here (or freed twice)");
+  if (it == live_.end()) {
+    const auto p = reinterpret_cast<std::uintptr_t>(a.ptr);
+    for (const Slab& s : slabs_) {
+      const auto base = reinterpret_cast<std::uintptr_t>(s.base);
+      if (s.base && p >= base && p < base + s.bytes)
+        return FailedPreconditionError(
+            "BuddyAllocator::deallocate: the block at this pointer is not live (double free)");
+    }
+    return InvalidArgumentError("BuddyAllocator::deallocate: pointer was not allocated here");
+  }
   const Live l = it->second;
+  if (a.slab_id != l.slab || a.block_id != static_cast<std::uint32_t>(l.offset >> min_order_))
+    return InvalidArgumentError("BuddyAllocator::deallocate: slab_id " + std::to_string(a.slab_id) +
+                                " / block_id " + std::to_string(a.block_id) +
+                                " do not name the live block at this pointer");
   live_.erase(it);
   stats_.bytes_in_use -= std::size_t{1} << l.order;
   stats_.bytes_requested -= l.requested;

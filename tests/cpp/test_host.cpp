@@ -8,6 +8,7 @@
 // (exact bytes, unsafe arm flagged by the race verifier, random-DAG fuzz) and the
 // buddy allocator on host memory with fake streams.  Expected values are derived
 // in the comments next to each check.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -729,7 +730,140 @@ TEST(buddy_growth_bypass_and_trim) {
   CHECK_EQ(b.stats().bytes_reserved, std::size_t{1 << 20});
   CHECK_OK(b.validate());
   CHECK_OK(b.deallocate(*a, s1));
-  CHECK(b.deallocate(*a, s1).code() == StatusCode::kInvalidArgument);   // double free
+  CHECK(b.deallocate(*a, s1).code() == StatusCode::kFailedPrecondition);   // double free
+}
+
+// Handles that name no live block (the reference's test_buddy_bad_handles,
+// tests/test_host_core.cpp:717-748): a double free is a failed precondition; a
+// live pointer with the wrong slab or block id, or a pointer from elsewhere, an
+// invalid argument (and the block stays live); a null pointer is a no-op.
+TEST(buddy_bad_handles) {
+  HostBuddy b(small_cfg(ReusePolicy::kCoarseStreamPoll));
+  const auto s1 = fake_stream(1);
+  auto keep = b.allocate(4096, s1);
+  auto r = b.allocate(1024, s1);
+  CHECK(keep.ok() && r.ok());
+  Allocation bad = *keep;
+  bad.slab_id = 99;
+  CHECK(b.deallocate(bad, s1).code() == StatusCode::kInvalidArgument);
+  bad = *keep;
+  bad.block_id = 100000;
+  CHECK(b.deallocate(bad, s1).code() == StatusCode::kInvalidArgument);
+  CHECK_EQ(b.stats().bytes_in_use, std::size_t{4096 + 1024});   // both still live
+  CHECK_OK(b.deallocate(*r, s1));
+  CHECK(b.deallocate(*r, s1).code() == StatusCode::kFailedPrecondition);
+  std::vector<char> elsewhere(4096);
+  bad = *keep;
+  bad.ptr = elsewhere.data();
+  CHECK(b.deallocate(bad, s1).code() == StatusCode::kInvalidArgument);
+  bad.ptr = nullptr;
+  CHECK_OK(b.deallocate(bad, s1));                             // free(nullptr) convention
+  CHECK_OK(b.validate());
+  CHECK_OK(b.deallocate(*keep, s1));
+  CHECK_OK(b.validate());
+}
+
+// The rounding a block costs, pinned (the reference's test_buddy_internal_waste,
+// tests/test_host_core.cpp:537-565): each block is the next power of two, and the
+// stats add up the requests and the blocks.
+TEST(buddy_internal_waste) {
+  HostBuddy b(small_cfg(ReusePolicy::kCoarseStreamPoll));
+  const std::pair<std::size_t, std::size_t> cases[] = {{257, 512}, {768, 1024}, {3072, 4096},
+                                                       {4097, 8192}};
+  std::size_t ask = 0, blocks = 0;
+  std::vector<Allocation> live;
+  for (const auto& [want, block] : cases) {
+    auto r = b.allocate(want, fake_stream(1));
+    CHECK(r.ok());
+    CHECK_EQ(r->bytes, block);
+    CHECK_EQ(r->internal_waste(), block - want);
+    ask += want;
+    blocks += block;
+    live.push_back(*r);
+  }
+  const AllocatorStats st = b.stats();
+  CHECK_EQ(st.bytes_requested, ask);
+  CHECK_EQ(st.bytes_in_use, blocks);
+  CHECK_EQ(st.internal_waste(), blocks - ask);
+  for (const Allocation& a : live) CHECK_OK(b.deallocate(a, fake_stream(1)));
+  CHECK_EQ(b.stats().internal_waste(), std::size_t{0});
+}
+
+// Random churn with ground truth the test keeps itself (the reference's
+// test_buddy_property_no_overlap, tests/test_host_core.cpp:436-535): every block is
+// aligned and large enough, no two live blocks overlap, and a byte pattern written
+// over each block's whole usable size is intact when it is freed (which bookkeeping
+// that only agrees with itself would not show).  The slabs are host memory here;
+// where a block lives is the allocator's integer arithmetic either way.
+template <class A, class SizeFn>
+static void churn_no_overlap(A& alloc, SizeFn size_of, std::size_t block_floor, int iters,
+                             std::uint64_t seed) {
+  struct LiveBlock {
+    Allocation a;
+    rt::StreamHandle s;
+    unsigned char magic;
+  };
+  std::vector<LiveBlock> live;
+  std::uint64_t rng = seed;
+  auto next = [&] { rng = rng * 6364136223846793005ULL + 1442695040888963407ULL; return rng >> 33; };
+  std::size_t in_use = 0, requested = 0;
+  int overlap = 0, magic = 0, shape = 0;
+  for (int it = 0; it < iters; ++it) {
+    if (live.empty() || next() % 100 < 60) {
+      const std::size_t want = size_of(next());
+      const auto s = fake_stream(1 + next() % 2);
+      auto r = alloc.allocate(want, s);
+      CHECK(r.ok());
+      if (!r.ok()) continue;
+      if (r->bytes < want || r->bytes < block_floor || r->requested_bytes != want ||
+          reinterpret_cast<std::uintptr_t>(r->ptr) % 256 != 0)
+        ++shape;
+      const auto m = static_cast<unsigned char>(1 + it % 251);
+      std::memset(r->ptr, m, r->bytes);
+      live.push_back({*r, s, m});
+      in_use += r->bytes;
+      requested += want;
+    } else {
+      const std::size_t i = next() % live.size();
+      const LiveBlock l = live[i];
+      const auto* p = static_cast<const unsigned char*>(l.a.ptr);
+      for (std::size_t k = 0; k < l.a.bytes; ++k)
+        if (p[k] != l.magic) {
+          ++magic;
+          break;
+        }
+      CHECK_OK(alloc.deallocate(l.a, l.s));
+      live.erase(live.begin() + static_cast<std::ptrdiff_t>(i));
+      in_use -= l.a.bytes;
+      requested -= l.a.requested_bytes;
+    }
+    if (it % 97 == 0) {
+      std::vector<std::pair<std::uintptr_t, std::uintptr_t>> iv;
+      for (const LiveBlock& l : live)
+        iv.emplace_back(reinterpret_cast<std::uintptr_t>(l.a.ptr),
+                        reinterpret_cast<std::uintptr_t>(l.a.ptr) + l.a.bytes);
+      std::sort(iv.begin(), iv.end());
+      for (std::size_t k = 1; k < iv.size(); ++k)
+        if (iv[k].first < iv[k - 1].second) ++overlap;
+      CHECK_OK(alloc.validate());
+    }
+    CHECK_EQ(alloc.stats().bytes_in_use, in_use);
+    CHECK_EQ(alloc.stats().bytes_requested, requested);
+  }
+  CHECK_EQ(overlap, 0);
+  CHECK_EQ(magic, 0);
+  CHECK_EQ(shape, 0);
+  for (const LiveBlock& l : live) CHECK_OK(alloc.deallocate(l.a, l.s));
+  CHECK_EQ(alloc.stats().bytes_in_use, std::size_t{0});
+  CHECK_OK(alloc.validate());
+}
+
+TEST(buddy_property_no_overlap) {
+  for (ReusePolicy pol : {ReusePolicy::kSameStreamOnly, ReusePolicy::kCoarseStreamPoll}) {
+    HostBuddy b(small_cfg(pol));
+    const std::size_t sizes[] = {1, 255, 256, 257, 768, 3072, 4097, 8192, 100000};
+    churn_no_overlap(b, [&](std::uint64_t r) { return sizes[r % 9]; }, 256, 20000, 0x1234567);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -916,6 +1050,70 @@ TEST(freelist_bypass_trim_and_random_walk) {
   auto fresh = f.allocate(4096, s1);                          // a new slab after the trim
   CHECK(fresh.ok());
   CHECK_OK(f.deallocate(*fresh, s1));
+}
+
+TEST(freelist_property_no_overlap) {
+  for (ReusePolicy pol : {ReusePolicy::kSameStreamOnly, ReusePolicy::kCoarseStreamPoll}) {
+    HostFreeList f(fl_cfg(pol));
+    const std::size_t sizes[] = {1, 100, 512, 513, 4096, 65536, 65537, 300000, 1 << 20};
+    churn_no_overlap(f, [&](std::uint64_t r) { return sizes[r % 9]; }, 512, 20000, 0x7654321);
+  }
+}
+
+// The defining difference, head to head (the reference's test_freelist_no_coalescing,
+// tests/test_host_core.cpp:962-1010): carve a whole slab into 512 B blocks and free
+// two adjacent ones.  Buddy merges them into a 1 KiB block that a 1 KiB request
+// reuses in place; FreeList keeps two 512 B blocks, so a 1 KiB request needs a new
+// slab.
+TEST(freelist_no_coalescing_vs_buddy) {
+  {
+    FreeListConfig c = fl_cfg(ReusePolicy::kCoarseStreamPoll);
+    c.slab_bytes = 64 << 10;
+    HostFreeList f(c);
+    std::vector<Allocation> live;
+    for (int i = 0; i < 128; ++i) {
+      auto x = f.allocate(512, fake_stream(1));
+      CHECK(x.ok());
+      live.push_back(*x);
+    }
+    CHECK_EQ(f.raw_allocs, 1);
+    CHECK_EQ(f.stats().largest_free_block, std::size_t{0});     // the slab is fully carved
+    CHECK(static_cast<char*>(live[1].ptr) == static_cast<char*>(live[0].ptr) + 512);
+    CHECK_OK(f.deallocate(live[0], fake_stream(1)));
+    CHECK_OK(f.deallocate(live[1], fake_stream(1)));
+    CHECK_OK(f.settle_pending());
+    CHECK_EQ(f.stats().largest_free_block, std::size_t{512});   // not merged
+    auto k = f.allocate(1024, fake_stream(1));
+    CHECK(k.ok() && k->ptr != live[0].ptr);
+    CHECK_EQ(f.raw_allocs, 2);
+    CHECK_OK(f.validate());
+    CHECK_OK(f.deallocate(*k, fake_stream(1)));
+    for (std::size_t i = 2; i < live.size(); ++i) CHECK_OK(f.deallocate(live[i], fake_stream(1)));
+  }
+  {
+    BuddyConfig c = small_cfg(ReusePolicy::kCoarseStreamPoll);
+    c.initial_slab_bytes = 64 << 10;
+    HostBuddy b(c);
+    std::vector<Allocation> live;
+    for (int i = 0; i < 128; ++i) {
+      auto x = b.allocate(512, fake_stream(1));
+      CHECK(x.ok());
+      live.push_back(*x);
+    }
+    CHECK_EQ(b.raw_allocs, 1);
+    CHECK_EQ(b.stats().largest_free_block, std::size_t{0});
+    CHECK(static_cast<char*>(live[1].ptr) == static_cast<char*>(live[0].ptr) + 512);
+    CHECK_OK(b.deallocate(live[0], fake_stream(1)));
+    CHECK_OK(b.deallocate(live[1], fake_stream(1)));
+    CHECK_OK(b.settle_pending());
+    CHECK_EQ(b.stats().largest_free_block, std::size_t{1024});  // the two buddies merged
+    auto k = b.allocate(1024, fake_stream(1));
+    CHECK(k.ok() && k->ptr == live[0].ptr);
+    CHECK_EQ(b.raw_allocs, 1);
+    CHECK_OK(b.validate());
+    CHECK_OK(b.deallocate(*k, fake_stream(1)));
+    for (std::size_t i = 2; i < live.size(); ++i) CHECK_OK(b.deallocate(live[i], fake_stream(1)));
+  }
 }
 
 TEST(first_bit_mismatch_helper) {
