@@ -27,6 +27,7 @@
 #include "mcke/kernels/softmax_online.hpp"
 #include "mcke/memory/buddy_allocator.hpp"
 #include "mcke/memory/freelist_allocator.hpp"
+#include "mcke/profiling/host_timer.hpp"
 #include "mcke/profiling/profiler.hpp"
 
 using namespace mcke;
@@ -1114,6 +1115,76 @@ TEST(freelist_no_coalescing_vs_buddy) {
     CHECK_OK(b.deallocate(*k, fake_stream(1)));
     for (std::size_t i = 2; i < live.size(); ++i) CHECK_OK(b.deallocate(live[i], fake_stream(1)));
   }
+}
+
+// Nearest-rank percentiles at the sizes where an off-by-one hides (the reference's
+// test_latency_stats_edge_cases, tests/test_host_core.cpp:1194-1256), the histogram's
+// buckets, and a self-consistent clock calibration.
+TEST(latency_stats_nearest_rank_and_calibration) {
+  {
+    LatencyStats s(1);
+    s.add(777);
+    s.finalize();
+    for (double p : {0.0, 50.0, 99.9, 100.0}) CHECK_EQ(s.percentile(p), std::uint64_t{777});
+    CHECK_EQ(s.min(), std::uint64_t{777});
+    CHECK_EQ(s.max(), std::uint64_t{777});
+  }
+  {
+    LatencyStats s(2);
+    s.add(20);
+    s.add(10);
+    s.finalize();
+    CHECK_EQ(s.percentile(0.0), std::uint64_t{10});
+    CHECK_EQ(s.percentile(100.0), std::uint64_t{20});
+    CHECK_EQ(s.median(), std::uint64_t{10});                 // rank ceil(0.5 * 2) = 1: the lower
+  }
+  {
+    LatencyStats s(5);
+    for (int i = 0; i < 5; ++i) s.add(42);
+    s.finalize();
+    CHECK_EQ(s.median(), std::uint64_t{42});
+    CHECK_EQ(s.p99(), std::uint64_t{42});
+    CHECK(std::fabs(s.mean_ns() - 42.0) < 1e-9);
+  }
+  {
+    LatencyStats s(100);
+    for (int i = 100; i >= 1; --i) s.add(static_cast<std::uint64_t>(i));
+    CHECK(!s.is_finalized());
+    s.finalize();
+    CHECK(s.is_finalized());
+    CHECK_EQ(s.percentile(1.0), std::uint64_t{1});
+    CHECK_EQ(s.median(), std::uint64_t{50});
+    CHECK_EQ(s.p90(), std::uint64_t{90});
+    CHECK_EQ(s.p99(), std::uint64_t{99});
+    CHECK_EQ(s.p999(), std::uint64_t{100});                  // rank ceil(99.9) = 100
+    CHECK_EQ(s.percentile(100.0), std::uint64_t{100});
+    CHECK(std::fabs(s.mean_ns() - 50.5) < 1e-9);
+    // Buckets of a 10 ns floor: [0,10] holds 1..10, (10,20] 11..20, (20,40],
+    // (40,80], (80,160] the rest.
+    CHECK(s.log2_histogram(10) == "    <= 10 ns: 10\n    <= 20 ns: 10\n    <= 40 ns: 20\n"
+                                  "    <= 80 ns: 40\n    <= 160 ns: 20\n");
+  }
+  {
+    LatencyStats s(0);
+    s.finalize();
+    CHECK(s.empty());
+    CHECK_EQ(s.count(), std::size_t{0});
+    CHECK_EQ(s.median(), std::uint64_t{0});
+    CHECK_EQ(s.max(), std::uint64_t{0});
+    CHECK(s.mean_ns() == 0.0);
+    CHECK(s.log2_histogram(10) == "  (no samples)\n");
+  }
+  const ClockCalibration cal = ClockCalibration::measure(20000);
+  CHECK(cal.floor_ns > 0);
+  CHECK(cal.floor_ns >= cal.tick_ns && cal.floor_ns >= cal.paired_median_ns);
+  CHECK(cal.is_below_floor(cal.floor_ns));
+  CHECK(!cal.is_below_floor(cal.floor_ns * 1000));
+  CHECK(!cal.describe().empty());
+  HostTimer t;
+  t.start();
+  volatile double sink = 0;
+  for (int i = 0; i < 100000; ++i) sink = sink + std::sqrt(static_cast<double>(i));
+  CHECK(t.stop_ns() > 0);
 }
 
 TEST(first_bit_mismatch_helper) {
