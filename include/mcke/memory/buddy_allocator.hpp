@@ -100,6 +100,7 @@ class BuddyAllocator : public DeviceAllocator {
   };
 
   [[nodiscard]] unsigned order_for(std::size_t bytes) const;
+  [[nodiscard]] std::uint32_t node_id(std::uint32_t slab, std::size_t offset, unsigned order) const;
   [[nodiscard]] StatusOr<std::uint32_t> add_slab(std::size_t min_bytes);
   [[nodiscard]] bool try_take(unsigned order, std::uint32_t* slab, std::size_t* offset);
   void release_block(std::uint32_t slab, std::size_t offset, unsigned order);

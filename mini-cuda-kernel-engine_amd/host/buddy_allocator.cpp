@@ -9,6 +9,7 @@
 #include <string>
 
 #include "mcke/core/device.hpp"
+#include "mcke/memory/buddy_math.hpp"
 
 namespace mcke {
 
@@ -164,6 +165,13 @@ void BuddyAllocator::drain_all_blocking() {
   parked_.clear();
 }
 
+// The block's node in heap order over its slab's tree (buddy_math.hpp): level
+// top_order - order, index offset >> order within the level.
+std::uint32_t BuddyAllocator::node_id(std::uint32_t slab, std::size_t offset, unsigned order) const {
+  const unsigned top = slabs_[slab].top_order;
+  return static_cast<std::uint32_t>(buddy::node_at(offset, top - order, top));
+}
+
 StatusOr<Allocation> BuddyAllocator::allocate(std::size_t bytes, rt::StreamHandle stream) {
   ++stats_.alloc_calls;
   if (bytes == 0) return InvalidArgumentError("BuddyAllocator::allocate: zero bytes");
@@ -218,7 +226,7 @@ StatusOr<Allocation> BuddyAllocator::allocate(std::size_t bytes, rt::StreamHandl
   a.bytes = block;
   a.requested_bytes = bytes;
   a.slab_id = slab;
-  a.block_id = static_cast<std::uint32_t>(off >> min_order_);
+  a.block_id = node_id(slab, off, order);
   return a;
 }
 
@@ -250,7 +258,7 @@ Status BuddyAllocator::deallocate(const Allocation& a, rt::StreamHandle stream) 
     return InvalidArgumentError("BuddyAllocator::deallocate: pointer was not allocated here");
   }
   const Live l = it->second;
-  if (a.slab_id != l.slab || a.block_id != static_cast<std::uint32_t>(l.offset >> min_order_))
+  if (a.slab_id != l.slab || a.block_id != node_id(l.slab, l.offset, l.order))
     return InvalidArgumentError("BuddyAllocator::deallocate: slab_id " + std::to_string(a.slab_id) +
                                 " / block_id " + std::to_string(a.block_id) +
                                 " do not name the live block at this pointer");

@@ -26,6 +26,7 @@
 #include "mcke/kernels/kernels.hpp"
 #include "mcke/kernels/softmax_online.hpp"
 #include "mcke/memory/buddy_allocator.hpp"
+#include "mcke/memory/buddy_math.hpp"
 #include "mcke/memory/freelist_allocator.hpp"
 #include "mcke/profiling/host_timer.hpp"
 #include "mcke/profiling/profiler.hpp"
@@ -1104,6 +1105,11 @@ TEST(freelist_no_coalescing_vs_buddy) {
     CHECK_EQ(b.raw_allocs, 1);
     CHECK_EQ(b.stats().largest_free_block, std::size_t{0});
     CHECK(static_cast<char*>(live[1].ptr) == static_cast<char*>(live[0].ptr) + 512);
+    // block_id is the node in heap order over the 64 KiB slab's tree: the first two
+    // 512 B blocks are the leftmost leaves of level 7, siblings.
+    CHECK_EQ(live[0].block_id, static_cast<std::uint32_t>(buddy::heap_index(7, 0)));
+    CHECK_EQ(static_cast<std::size_t>(live[1].block_id), buddy::buddy_of(live[0].block_id));
+    CHECK_EQ(buddy::offset_of(live[127].block_id, 16), std::size_t{127 * 512});
     CHECK_OK(b.deallocate(live[0], fake_stream(1)));
     CHECK_OK(b.deallocate(live[1], fake_stream(1)));
     CHECK_OK(b.settle_pending());
@@ -1185,6 +1191,43 @@ TEST(latency_stats_nearest_rank_and_calibration) {
   volatile double sink = 0;
   for (int i = 0; i < 100000; ++i) sink = sink + std::sqrt(static_cast<double>(i));
   CHECK(t.stop_ns() > 0);
+}
+
+// The tree arithmetic at run time as well as at compile time: every node of a
+// 12-level tree round-trips through (level, index) and offset, children and
+// buddies are consistent, and level_for_size picks the smallest block that holds a
+// request (the reference's test_buddy_math / test_buddy_geometry).
+TEST(buddy_math_tree_arithmetic) {
+  using namespace buddy;
+  CHECK(is_power_of_two(1) && is_power_of_two(4096) && !is_power_of_two(0) && !is_power_of_two(768));
+  CHECK_EQ(align_up(257, 256), std::size_t{512});
+  CHECK_EQ(align_up(512, 256), std::size_t{512});
+  const unsigned arena = 20, minb = 8, L = max_level(arena, minb);
+  CHECK_EQ(L, 12u);
+  CHECK_EQ(node_count(L), (std::size_t{1} << 13) - 1);
+  for (std::size_t n = 0; n < node_count(L); ++n) {
+    const unsigned lv = level_of(n);
+    CHECK(heap_index(lv, index_in_level(n)) == n);
+    CHECK(index_in_level(n) < nodes_at_level(lv));
+    CHECK(node_at(offset_of(n, arena), lv, arena) == n);
+    CHECK(offset_of(n, arena) % block_bytes_at_level(arena, lv) == 0);
+    if (!is_root(n)) {
+      CHECK(buddy_of(buddy_of(n)) == n && parent_of(buddy_of(n)) == parent_of(n));
+      CHECK((offset_of(n, arena) ^ block_bytes_at_level(arena, lv)) == offset_of(buddy_of(n), arena));
+    }
+    if (lv < L) {
+      CHECK(parent_of(left_child_of(n)) == n && parent_of(right_child_of(n)) == n);
+      CHECK(offset_of(left_child_of(n), arena) == offset_of(n, arena));
+    }
+  }
+  for (std::size_t bytes : {std::size_t{1}, std::size_t{255}, std::size_t{256}, std::size_t{257},
+                            std::size_t{4097}, std::size_t{1} << 19, (std::size_t{1} << 19) + 1,
+                            std::size_t{1} << 20}) {
+    const unsigned lv = level_for_size(bytes, arena, minb);
+    CHECK(block_bytes_at_level(arena, lv) >= bytes);
+    CHECK(lv == L || block_bytes_at_level(arena, lv + 1) < std::max(bytes, std::size_t{256}));
+  }
+  CHECK_EQ(level_for_size((std::size_t{1} << 20) + 1, arena, minb), L + 1);
 }
 
 TEST(first_bit_mismatch_helper) {
