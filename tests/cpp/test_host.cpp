@@ -11,14 +11,19 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <random>
 #include <set>
+#include <string>
+
+#include <unistd.h>
 
 #include "check.hpp"
 #include "../../mini-cuda-kernel-engine_amd/csrc/fast_div.hpp"
+#include "mcke/graph/cost_model.hpp"
 #include "mcke/graph/executor.hpp"
 #include "mcke/graph/graph.hpp"
 #include "mcke/graph/memory_plan.hpp"
@@ -336,6 +341,83 @@ TEST(op_costs_are_the_ideal_formulas) {
   const Roofline rl = mi355x_roofline();
   CHECK(!rl.memory_bound(g.arithmetic_intensity()) && rl.memory_bound(ba.arithmetic_intensity()));
   CHECK(std::fabs(rl.ridge_point_ai() - 157.3e12 / 8e12) < 1e-9);
+}
+
+// The roofline cost model that balances streams (the reference's
+// test_cost_model_roofline, tests/test_graph_host.cpp:816-858), on MI355X's
+// published figures: a 4096^3 GEMM is 1.374e11 flops / 157.3e12 = 0.874 ms of
+// arithmetic against 201 MB / 8e12 = 0.025 ms of traffic (compute-bound); softmax
+// 8192 x 4096 is 2.68e8 B / 8e12 = 0.0336 ms of traffic against 1.68e8 flops /
+// 157.3e12 = 0.0011 ms (memory-bound).  A zero roofline costs 0, not infinity.
+TEST(cost_model_roofline) {
+  const Roofline rl = mi355x_roofline();
+  const OpCost gc = GemmOp(GemmParams{}).cost({Shape{4096, 4096}, Shape{4096, 4096}});
+  const double g_ms = plan_cost_ms(gc, rl);
+  CHECK(std::fabs(g_ms - 2.0 * 4096.0 * 4096.0 * 4096.0 / 157.3e12 * 1e3) < 1e-9);
+  CHECK(!op_is_memory_bound(gc, rl));
+  const OpCost sc = SoftmaxOp(SoftmaxParams{}).cost({Shape{8192, 4096}});
+  const double s_ms = plan_cost_ms(sc, rl);
+  CHECK(std::fabs(s_ms - 2.0 * 8192.0 * 4096.0 * 4.0 / 8e12 * 1e3) < 1e-12);
+  CHECK(op_is_memory_bound(sc, rl));
+  CHECK(g_ms / s_ms > 20.0);
+  const Roofline zero{};
+  CHECK(plan_cost_ms(gc, zero) == 0.0);
+  CHECK(zero.attainable_tflops(1.0) == 0.0 && zero.ridge_point_ai() == 0.0);
+}
+
+// Profiler::summary_table keeps three decimals on every row, not only the first
+// (the reference's test_summary_table_precision, tests/test_host_core.cpp:2448-2483:
+// a sticky setprecision(1) from the %peak column once cut rows 2.. to one
+// decimal), with its frozen column widths; write_csv writes the reference's
+// 13 columns (src/core/profiler.cpp:95-113) with each derived column computed
+// from the record.
+TEST(profiler_summary_table_and_csv) {
+  Profiler prof;
+  KernelRecord a;
+  a.name = "k";
+  a.variant = "first";
+  a.median_ms = 1.23456;
+  a.min_ms = 1.11111;
+  a.flops = 100;
+  a.bytes = 400;
+  a.iterations = 20;
+  KernelRecord b = a;
+  b.variant = "second";
+  b.median_ms = 0.52349;
+  b.min_ms = 0.51237;
+  prof.add(a);
+  prof.add(b);
+  Roofline rl;
+  rl.peak_gb_s = 235.4;
+  rl.peak_tflops = 8.130;
+  const std::string t = prof.summary_table(rl);
+  for (const char* s : {"1.235", "1.111", "0.523", "0.512"}) CHECK(t.find(s) != std::string::npos);
+  CHECK(t.find(std::string(117, '-')) != std::string::npos);
+  // A data row: 22 + 30 + 10 + 10 + 10 + 10 + 8 + 10 characters, then "  memory".
+  const std::size_t row2 = t.find("k     ", t.find("first"));
+  CHECK(row2 != std::string::npos);
+  const std::string line = t.substr(row2, t.find('\n', row2) - row2);
+  CHECK(line.size() == 110 + 8 && line.substr(110) == "  memory");
+  CHECK(line.substr(22, 6) == "second");
+
+  const std::string path = "/tmp/mcke_test_profiler_" + std::to_string(::getpid()) + ".csv";
+  CHECK_OK(prof.write_csv(path, rl));
+  std::FILE* f = std::fopen(path.c_str(), "r");
+  CHECK(f != nullptr);
+  std::string text;
+  char chunk[512];
+  while (std::size_t got = std::fread(chunk, 1, sizeof chunk, f)) text.append(chunk, got);
+  std::fclose(f);
+  std::remove(path.c_str());
+  // Default stream precision (6 significant digits): 400 B / 1.23456 ms = 0.000324002 GB/s,
+  // 100 flops -> 8.1e-08 TFLOP/s; AI 0.25 < ridge 34.5 -> memory; attainable
+  // 0.25 x 235.4 GB/s = 0.05885 TFLOP/s; efficiency 8.10005e-08 / 0.05885 = 1.37639e-04 %.
+  CHECK(text ==
+        "kernel,variant,median_ms,min_ms,iterations,ideal_flops,ideal_bytes,achieved_gb_s,"
+        "achieved_tflops,arithmetic_intensity,attainable_tflops,efficiency_pct,bound\n"
+        "k,first,1.23456,1.11111,20,100,400,0.000324002,8.10005e-08,0.25,0.05885,0.000137639,memory\n"
+        "k,second,0.52349,0.51237,20,100,400,0.000764102,1.91026e-07,0.25,0.05885,0.000324597,memory\n");
+  CHECK(!prof.write_csv("/nonexistent-dir/x.csv", rl).ok());
 }
 
 // ---------------------------------------------------------------------------
