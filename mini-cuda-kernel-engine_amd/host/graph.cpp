@@ -83,8 +83,8 @@ StatusOr<std::vector<TensorId>> Graph::add_node(OpPtr op, std::vector<TensorId> 
   for (std::size_t i = 0; i < inputs.size(); ++i) {
     if (inputs[i] >= tensors_.size()) {
       std::ostringstream os;
-      os << who << ": operand " << i << " names tensor " << inputs[i] << "; tensors 0.."
-         << tensors_.size() << " exist";
+      os << who << ": operand " << i << " is tensor id " << inputs[i] << ", but the graph holds "
+         << tensors_.size() << " tensors";
       return InvalidArgumentError(os.str());
     }
     in_shapes.push_back(tensors_[inputs[i]].shape);
@@ -251,7 +251,9 @@ std::vector<NodeId> Graph::dead_nodes() const {
 }
 
 // def_pos: position of the producer in `order` (-1 for graph inputs); last_use_pos:
-// position of the last reader, order.size() for graph outputs, and never below def_pos.
+// position of the last reader, never below def_pos, and order.size() for graph inputs
+// and outputs, which live through the whole run: an input is filled by set_input()
+// outside the plan and read again on every run (reference graph.hpp:71-81).
 std::vector<Graph::LiveRange> Graph::compute_live_ranges(const std::vector<NodeId>& order) const {
   std::vector<LiveRange> ranges(tensors_.size());
   for (int pos = 0; pos < static_cast<int>(order.size()); ++pos) {
@@ -264,7 +266,8 @@ std::vector<Graph::LiveRange> Graph::compute_live_ranges(const std::vector<NodeI
   for (std::size_t t = 0; t < tensors_.size(); ++t) {
     LiveRange& r = ranges[t];
     if (tensors_[t].is_graph_input) r.def_pos = -1;
-    if (tensors_[t].is_graph_output) r.last_use_pos = static_cast<int>(order.size());
+    if (tensors_[t].is_graph_input || tensors_[t].is_graph_output)
+      r.last_use_pos = static_cast<int>(order.size());
     r.last_use_pos = std::max(r.last_use_pos, r.def_pos);
   }
   return ranges;
