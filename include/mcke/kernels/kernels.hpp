@@ -105,6 +105,19 @@ enum class SoftmaxVariant : std::uint8_t { kThreePass, kOnlineOnePass };
                                                 static_cast<int>(variant), &t, stream));
 }
 
+// No reference counterpart: launch_gemm_f32 (kMfmaF32, beta = 0) and
+// launch_bias_act_f32 in one launch, y = act(alpha * A B + bias[col]), with the
+// bits of the two launches in sequence (mcke_launch_gemm_bias_act_f32).
+[[nodiscard]] inline Status launch_gemm_bias_act_f32(const float* a, const float* b,
+                                                    const float* bias, float* y, std::int64_t m,
+                                                    std::int64_t n, std::int64_t k, float alpha,
+                                                    Activation act, GemmTile tile,
+                                                    rt::StreamHandle stream) {
+  const mcke_gemm_tile t = detail::to_c(tile);
+  return detail::status_of(mcke_launch_gemm_bias_act_f32(a, b, bias, y, m, n, k, alpha,
+                                                         static_cast<int>(act), &t, stream));
+}
+
 struct GemmKernelAttrs {
   int regs_per_thread = 0;
   std::size_t static_smem_bytes = 0;

@@ -176,6 +176,20 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
                          int64_t k, float alpha, float beta, int variant,
                          const mcke_gemm_tile* tile, void* stream);
 
+/* No reference counterpart: launch_gemm_f32 (kMfmaF32, beta = 0) with
+ * launch_bias_act_f32 fused into the GEMM's epilogue,
+ *   y[i,j] = act(alpha * (A B)[i,j] + bias[j]),
+ * for callers that chain the two (the graph layer's GemmBiasAct node, the MLP
+ * block of the benchmark): C never goes to memory and one launch is saved.  The
+ * result has the bits of mcke_launch_gemm_f32(a, b, y, m, n, k, alpha, 0,
+ * MCKE_GEMM_MFMA_F32, tile) followed by mcke_launch_bias_act_f32(y, bias, y2, m, n,
+ * activation, ...).  Validation as mcke_launch_gemm_f32 for kMfmaF32, plus: bias
+ * (n floats, any alignment) must not be null, y must not alias a, b or bias, and
+ * activation is an mcke_activation value. */
+int mcke_launch_gemm_bias_act_f32(const float* a, const float* b, const float* bias, float* y,
+                                  int64_t m, int64_t n, int64_t k, float alpha, int activation,
+                                  const mcke_gemm_tile* tile, void* stream);
+
 /* gemm_kernel_attrs, kernels.hpp:301-302 / gemm.cu:884-904. */
 int mcke_gemm_kernel_attrs(int variant, const mcke_gemm_tile* tile,
                            mcke_kernel_attrs* out);

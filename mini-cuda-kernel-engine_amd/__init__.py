@@ -183,6 +183,9 @@ def lib() -> C.CDLL:
         "mcke_launch_row_softmax_f32": (C.c_int, [_VP, _VP, _I64, _I64, C.c_int, _VP]),
         "mcke_launch_gemm_f32": (C.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, C.c_float,
                                            C.c_float, C.c_int, C.POINTER(GemmTile), _VP]),
+        "mcke_launch_gemm_bias_act_f32": (C.c_int, [_VP, _VP, _VP, _VP, _I64, _I64, _I64,
+                                                    C.c_float, C.c_int, C.POINTER(GemmTile),
+                                                    _VP]),
         "mcke_gemm_kernel_attrs": (C.c_int, [C.c_int, C.POINTER(GemmTile),
                                              C.POINTER(KernelAttrs)]),
         "mcke_gemm_mfma_default_tile": (C.c_int, [_I64, _I64, _I64, C.POINTER(GemmTile)]),
@@ -506,6 +509,17 @@ def launch_gemm_f32(a, b, c, m: int, n: int, k: int, alpha: float, beta: float, 
     tile = GemmTile() if tile is None else tile
     return _st(lib().mcke_launch_gemm_f32(_ptr(a), _ptr(b), _ptr(c), m, n, k, alpha, beta,
                                           int(variant), C.byref(tile), _sh(stream)))
+
+
+def launch_gemm_bias_act_f32(a, b, bias, y, m: int, n: int, k: int, alpha: float, act,
+                             tile: GemmTile | None = None, stream=None) -> Status:
+    """y = act(alpha * A B + bias[col]) on kMfmaF32 with the bias and activation in
+    the GEMM's epilogue: the bits of launch_gemm_f32 (beta = 0) followed by
+    launch_bias_act_f32.  No reference counterpart (a fusion of its two launchers)."""
+    tile = gemm_mfma_default_tile(m, n, k) if tile is None else tile
+    return _st(lib().mcke_launch_gemm_bias_act_f32(_ptr(a), _ptr(b), _ptr(bias), _ptr(y), m, n,
+                                                   k, alpha, int(act), C.byref(tile),
+                                                   _sh(stream)))
 
 
 def gemm_kernel_attrs(variant, tile: GemmTile | None = None):

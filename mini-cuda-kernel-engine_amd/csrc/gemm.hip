@@ -238,7 +238,7 @@ int64_t device_cu_count() {
 
 using GemmFn = void (*)(const float*, const float*, float*, int, int, int, float, float);
 using MfmaFn = void (*)(const float*, const float*, float*, int, int, int, float, float, int,
-                        int);
+                        int, EpiArgs);
 
 // MFMA instantiations: (bm, bn, bk) with tm = bm/16, tn = bn/16 (256 lanes).
 // `even`: 16-byte path for M, N, K multiples of the tile (no bounds checks);
@@ -250,18 +250,24 @@ struct MfmaCfg {
   // `even` is the direct-to-LDS kernel, whose per-lane source offsets are 32-bit
   // byte offsets within a tile's BM rows of A and 32 rows of B.
   bool even_dma = false;
+  // The same three kernels with the fused bias + activation epilogue.
+  MfmaFn even_f = nullptr, vec_f = nullptr, scalar_f = nullptr;
 };
 
 #define MCKE_MFMA_CFG(BM, BN, BK)                                                     \
   {BM, BN, BK, &gemm_mfma_kernel<BM, BN, BK, true, true>,                            \
    &gemm_mfma_kernel<BM, BN, BK, true, false>, &gemm_mfma_kernel<BM, BN, BK, false, false>, \
-   kMfmaThreads}
+   kMfmaThreads, false, &gemm_mfma_kernel<BM, BN, BK, true, true, true>,             \
+   &gemm_mfma_kernel<BM, BN, BK, true, false, true>,                                  \
+   &gemm_mfma_kernel<BM, BN, BK, false, false, true>}
 // BK = 32 whole tiles take the direct-to-LDS kernel (ST stages, KS wave groups
 // splitting each stage's K range).
 #define MCKE_MFMA_CFG_DMA(BM, BN, ST, KS)                                             \
   {BM, BN, 32, &gemm_mfma_dma_kernel<BM, BN, ST, KS>,                                \
    &gemm_mfma_kernel<BM, BN, 32, true, false>, &gemm_mfma_kernel<BM, BN, 32, false, false>, \
-   kDmaThreads<BM, BN, KS>, true}
+   kDmaThreads<BM, BN, KS>, true, &gemm_mfma_dma_kernel<BM, BN, ST, KS, true>,        \
+   &gemm_mfma_kernel<BM, BN, 32, true, false, true>,                                  \
+   &gemm_mfma_kernel<BM, BN, 32, false, false, true>}
 
 // 64 x 64 tiles serve small problems, whose single round of tiles leaves one
 // workgroup per CU.  Their direct-to-LDS kernel meets at its barrier in the
@@ -292,6 +298,8 @@ struct Spec {
   GemmFn fn = nullptr;
   MfmaFn mfma = nullptr;
   MfmaFn mfma_even = nullptr;     // unchecked 16-byte variant for whole tiles
+  MfmaFn mfma_f = nullptr;        // the two with the fused bias + activation epilogue
+  MfmaFn mfma_even_f = nullptr;
   int even_threads = 0;           // their block size
   bool even_dma = false;          // they take 32-bit per-lane source offsets
   dim3 block{1, 1, 1};
@@ -353,6 +361,8 @@ int gemm_spec(int variant, const mcke_gemm_tile* tile, bool vec4, Spec& s) {
                        "(64,64,32,4,4) and (32,32,32,2,2); no fallback is applied");
       s.mfma = vec4 ? cfg->vec : cfg->scalar;
       s.mfma_even = vec4 ? cfg->even : nullptr;
+      s.mfma_f = vec4 ? cfg->vec_f : cfg->scalar_f;
+      s.mfma_even_f = vec4 ? cfg->even_f : nullptr;
       s.even_threads = cfg->even_threads;
       s.even_dma = cfg->even_dma;
       s.tile_k = cfg->bk;
@@ -409,6 +419,32 @@ int launch_rocblas(const float* a, const float* b, float* c, int m, int n, int k
   return ok();
 }
 
+// One kMfmaF32 launch: whole tiles take the direct-to-LDS kernel, other shapes the
+// staged one; `fused` picks the instantiations with the bias + activation
+// epilogue, which route shapes exactly as the plain ones do (so a fused launch
+// accumulates in the plain launch's order).
+int launch_mfma(const Spec& sp, bool fused, const float* a, const float* b, float* c, int64_t m,
+                int64_t n, int64_t k, float alpha, float beta, EpiArgs epi, hipStream_t s) {
+  const int64_t tiles_m = (m + sp.tile_m - 1) / sp.tile_m;
+  const int64_t tiles_n = (n + sp.tile_n - 1) / sp.tile_n;
+  if (tiles_m * tiles_n > 2147483647LL)
+    return invalid("launch_gemm_f32: too many tiles for one launch");
+  const bool whole = sp.mfma_even && m % sp.tile_m == 0 && n % sp.tile_n == 0 &&
+                     k % sp.tile_k == 0 &&
+                     (!sp.even_dma || (static_cast<int64_t>(sp.tile_m) * k < (int64_t{1} << 30) &&
+                                       static_cast<int64_t>(32) * n < (int64_t{1} << 30)));
+  MfmaFn fn = whole ? (fused ? sp.mfma_even_f : sp.mfma_even) : (fused ? sp.mfma_f : sp.mfma);
+  const dim3 block = whole ? dim3(static_cast<unsigned>(sp.even_threads), 1, 1) : sp.block;
+  if (tiles_m * tiles_n * static_cast<int64_t>(block.x) > int64_t{UINT32_MAX})
+    return invalid("launch_gemm_f32: tiles x lanes exceed the grid's 32-bit work size; use a "
+                   "larger tile");
+  fn<<<static_cast<unsigned>(tiles_m * tiles_n), block, 0, s>>>(
+      a, b, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), alpha, beta,
+      static_cast<int>(tiles_m), static_cast<int>(tiles_n), epi);
+  MCKE_LAUNCH_CHECK(fused ? "gemm_mfma_kernel (bias + activation)" : "gemm_mfma_kernel");
+  return ok();
+}
+
 }  // namespace
 }  // namespace mcke_amd
 
@@ -439,25 +475,7 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
   Spec sp;
   if (int rc = gemm_spec(variant, tile, vec4, sp)) return rc;
 
-  if (sp.mfma) {
-    const int64_t tiles_m = (m + sp.tile_m - 1) / sp.tile_m;
-    const int64_t tiles_n = (n + sp.tile_n - 1) / sp.tile_n;
-    if (tiles_m * tiles_n > 2147483647LL)
-      return invalid("launch_gemm_f32: too many tiles for one launch");
-    const bool whole = sp.mfma_even && m % sp.tile_m == 0 && n % sp.tile_n == 0 &&
-                       k % sp.tile_k == 0 &&
-                       (!sp.even_dma || (static_cast<int64_t>(sp.tile_m) * k < (int64_t{1} << 30) &&
-                                         static_cast<int64_t>(32) * n < (int64_t{1} << 30)));
-    MfmaFn fn = whole ? sp.mfma_even : sp.mfma;
-    const dim3 block = whole ? dim3(static_cast<unsigned>(sp.even_threads), 1, 1) : sp.block;
-    if (tiles_m * tiles_n * static_cast<int64_t>(block.x) > int64_t{UINT32_MAX})
-      return invalid("launch_gemm_f32: tiles x lanes exceed the grid's 32-bit work size; use a "
-                     "larger tile");
-    fn<<<static_cast<unsigned>(tiles_m * tiles_n), block, 0, s>>>(
-        a, b, c, mi, ni, ki, alpha, beta, static_cast<int>(tiles_m), static_cast<int>(tiles_n));
-    MCKE_LAUNCH_CHECK("gemm_mfma_kernel");
-    return ok();
-  }
+  if (sp.mfma) return launch_mfma(sp, false, a, b, c, m, n, k, alpha, beta, EpiArgs{nullptr, 0}, s);
 
   // grid.x walks C column tiles and grid.y C row tiles for every ladder kernel
   // (kNaiveUncoalesced only changes which lane index runs along a row).
@@ -470,6 +488,27 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
   sp.fn<<<grid, sp.block, 0, s>>>(a, b, c, mi, ni, ki, alpha, beta);
   MCKE_LAUNCH_CHECK("gemm kernel");
   return ok();
+}
+
+int mcke_launch_gemm_bias_act_f32(const float* a, const float* b, const float* bias, float* y,
+                                  int64_t m, int64_t n, int64_t k, float alpha, int activation,
+                                  const mcke_gemm_tile* tile, void* stream) {
+  if (m == 0 || n == 0) return ok();
+  if (m < 0 || n < 0 || k < 0) return invalid("launch_gemm_bias_act_f32: negative extent");
+  if (!a || !b || !bias || !y) return invalid("launch_gemm_bias_act_f32: null pointer");
+  if (y == a || y == b || y == bias)
+    return invalid("launch_gemm_bias_act_f32: the output aliases an input, which violates the "
+                   "__restrict__ contract");
+  if (activation < MCKE_ACT_NONE || activation > MCKE_ACT_GELU_TANH)
+    return invalid("launch_gemm_bias_act_f32: unknown Activation " + std::to_string(activation));
+  if (m > 2147483647LL || n > 2147483647LL || k > 2147483647LL)
+    return invalid("launch_gemm_bias_act_f32: extent exceeds INT32_MAX");
+  const bool vec4 = (k % 4 == 0) && (n % 4 == 0) && aligned(a, 16) && aligned(b, 16) &&
+                    aligned(y, 16);
+  Spec sp;
+  if (int rc = gemm_spec(MCKE_GEMM_MFMA_F32, tile, vec4, sp)) return rc;
+  return launch_mfma(sp, true, a, b, y, m, n, k, alpha, 0.0f, EpiArgs{bias, activation},
+                     static_cast<hipStream_t>(stream));
 }
 
 int mcke_gemm_kernel_attrs(int variant, const mcke_gemm_tile* tile, mcke_kernel_attrs* out) {

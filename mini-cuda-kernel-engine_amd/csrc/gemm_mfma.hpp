@@ -189,6 +189,64 @@ struct MfmaStage {
 // (wm, wn) of the workgroup's tile at (m0, n0) (C is not read when beta == 0).
 // Lane (h, c) holds, for MFMA tile (i, j) and accumulator register r, row
 // 8*(r/4) + 4h + r%4 of the tile's 32 rows and column NT*c + j of the wave's WN.
+// The epilogue's extra operands.  A plain GEMM ignores them; a fused launch
+// (FUSED = true, beta = 0) stores y = act(alpha * acc + bias[col]) instead of
+// alpha * acc: the same fp32 value of alpha * acc that a plain launch writes to C,
+// then the activation exactly as bias_act computes it from C -- so the fused
+// result has the bits of mcke_launch_gemm_f32 followed by mcke_launch_bias_act_f32.
+struct EpiArgs {
+  const float* bias;   // N values
+  int act;             // MCKE activation, 0 .. 3
+};
+
+// alpha * acc rounded to fp32 before the bias is added: the empty asm makes the
+// product a register value, so the compiler cannot contract it with the add
+// into one fused multiply-add (which the unfused pair, storing C in between, never
+// does).
+__device__ __forceinline__ float epi_round(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+template <int ACT> __device__ __forceinline__ float epi_act(float o, float b) {
+  return act_xb<ACT>(epi_round(o), b);
+}
+
+// mfma_store_c's fused form (beta = 0): the bias of a lane's NT columns is read
+// once, before its rows.
+template <int MT, int NT, bool VEC, int ACT>
+__device__ __forceinline__ void mfma_store_c_act(const f32x16 (&acc)[MT][NT],
+                                                 float* __restrict__ C, int M, int N, int m0,
+                                                 int n0, int wm, int wn, int h, int c,
+                                                 float alpha, const float* __restrict__ bias) {
+  constexpr int WM = 32 * MT, WN = 32 * NT;
+  const bool vec_store = VEC && (NT == 4) && ((N & 3) == 0);
+  const int col0 = n0 + wn * WN + NT * c;
+  float bj[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) bj[j] = col0 + j < N ? bias[col0 + j] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+      if (row >= M) continue;
+      float* crow = C + static_cast<int64_t>(row) * N;
+      float v[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) v[j] = epi_act<ACT>(alpha * acc[i][j][r], bj[j]);
+      if (vec_store && col0 + 3 < N) {
+        *reinterpret_cast<f32x4*>(crow + col0) =
+            f32x4{v[0], v[NT > 1 ? 1 : 0], v[NT > 2 ? 2 : 0], v[NT > 3 ? 3 : 0]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          if (col0 + j < N) crow[col0 + j] = v[j];
+      }
+    }
+  }
+}
+
 template <int MT, int NT, bool VEC>
 __device__ __forceinline__ void mfma_store_c(const f32x16 (&acc)[MT][NT],
                                              float* __restrict__ C, int M, int N, int m0, int n0,
@@ -300,6 +358,87 @@ __device__ __forceinline__ void mfma_store_c_whole(const f32x16 (&acc)[MT][NT],
   }
 }
 
+// mfma_store_c_whole's fused form (beta = 0), the same stores.
+template <int MT, int NT, int ACT>
+__device__ __forceinline__ void mfma_store_c_whole_act(const f32x16 (&acc)[MT][NT],
+                                                       float* __restrict__ C, int N, int m0,
+                                                       int n0, int wm, int wn, int h, int c,
+                                                       float alpha,
+                                                       const float* __restrict__ bias) {
+  constexpr int WM = 32 * MT, WN = 32 * NT;
+  if constexpr (NT == 1) {
+    const int t = c & 3;
+    const int col = n0 + wn * WN + (c & ~3);
+    const float b0 = bias[col], b1 = bias[col + 1], b2 = bias[col + 2], b3 = bias[col + 3];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v0 = acc[i][0][4 * q], v1 = acc[i][0][4 * q + 1], v2 = acc[i][0][4 * q + 2],
+              v3 = acc[i][0][4 * q + 3];
+        quad_transpose(v0, v1, v2, v3, t);
+        const int row = m0 + wm * WM + i * 32 + 8 * q + 4 * h + t;
+        *reinterpret_cast<f32x4*>(C + static_cast<int64_t>(row) * N + col) =
+            f32x4{epi_act<ACT>(alpha * v0, b0), epi_act<ACT>(alpha * v1, b1),
+                  epi_act<ACT>(alpha * v2, b2), epi_act<ACT>(alpha * v3, b3)};
+      }
+    }
+  } else if constexpr (NT == 2) {
+    const int col = n0 + wn * WN + 2 * c;
+    const float b0 = bias[col], b1 = bias[col + 1];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        *reinterpret_cast<f32x2*>(C + static_cast<int64_t>(row) * N + col) =
+            f32x2{epi_act<ACT>(alpha * acc[i][0][r], b0), epi_act<ACT>(alpha * acc[i][1][r], b1)};
+      }
+    }
+  } else {
+    static_assert(NT == 4, "wave tiles are 1, 2 or 4 MFMA tiles wide");
+    const int col = n0 + wn * WN + 4 * c;
+    const float b0 = bias[col], b1 = bias[col + 1], b2 = bias[col + 2], b3 = bias[col + 3];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        *reinterpret_cast<f32x4*>(C + static_cast<int64_t>(row) * N + col) =
+            f32x4{epi_act<ACT>(alpha * acc[i][0][r], b0), epi_act<ACT>(alpha * acc[i][1][r], b1),
+                  epi_act<ACT>(alpha * acc[i][2][r], b2), epi_act<ACT>(alpha * acc[i][3][r], b3)};
+      }
+    }
+  }
+}
+
+// The store at a kernel's end: plain, or fused with the activation picked once
+// (a uniform branch around four copies of the store loop).
+template <int MT, int NT, bool VEC, bool WHOLE, bool FUSED>
+__device__ __forceinline__ void mfma_epilogue(const f32x16 (&acc)[MT][NT], float* __restrict__ C,
+                                              int M, int N, int m0, int n0, int wm, int wn, int h,
+                                              int c, float alpha, float beta, EpiArgs epi) {
+  if constexpr (!FUSED) {
+    if constexpr (WHOLE)
+      mfma_store_c_whole<MT, NT>(acc, C, N, m0, n0, wm, wn, h, c, alpha, beta);
+    else
+      mfma_store_c<MT, NT, VEC>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
+  } else {
+    auto store = [&]<int ACT>() {
+      if constexpr (WHOLE)
+        mfma_store_c_whole_act<MT, NT, ACT>(acc, C, N, m0, n0, wm, wn, h, c, alpha, epi.bias);
+      else
+        mfma_store_c_act<MT, NT, VEC, ACT>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, epi.bias);
+    };
+    switch (epi.act) {
+      case kActNone: store.template operator()<kActNone>(); break;
+      case kActRelu: store.template operator()<kActRelu>(); break;
+      case kActGeluErf: store.template operator()<kActGeluErf>(); break;
+      default: store.template operator()<kActGeluTanh>(); break;
+    }
+  }
+}
+
 template <int BM, int BN, int BK>
 struct MfmaVecIO {
   using S = MfmaStage<BM, BN, BK, true>;
@@ -357,10 +496,10 @@ template <int BN> constexpr int kMfmaWaveCols = BN >= 64 ? 2 : 1;
 template <int BM, int BN, int KS>
 constexpr int kDmaThreads = kWave * kMfmaWaveRows<BM> * kMfmaWaveCols<BN> * KS;
 
-template <int BM, int BN, int BK, bool VEC, bool EVEN>
+template <int BM, int BN, int BK, bool VEC, bool EVEN, bool FUSED = false>
 __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
-    int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
+    int N, int K, float alpha, float beta, int tiles_m, int tiles_n, EpiArgs epi) {
   // The 256 lanes form one 2 x 2 wave grid for tiles of 64 and more; a 32 x 32
   // tile is one wave wide and high, and its 4 waves are 4 groups splitting each
   // stage's K range, folded in group order at the end.
@@ -521,7 +660,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemm_mfma_kernel(
           for (int r = 0; r < 16; ++r) acc[i][j][r] += smem[slot(g, i, j, r)];
   }
 
-  mfma_store_c<MT, NT, VEC>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta);
+  mfma_epilogue<MT, NT, VEC, false, FUSED>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta, epi);
 }
 
 
@@ -586,10 +725,10 @@ __device__ __forceinline__ void mfma_dma_issue(int a_floats, const uint32_t (&of
 // one wave wide and high, uses it to give its workgroup four waves.  The sum
 // order over K differs from KS = 1 (the groups' partials are added last), and is
 // fixed for a given KS.
-template <int BM, int BN, int STAGES, int KS = 1>
+template <int BM, int BN, int STAGES, int KS = 1, bool FUSED = false>
 __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
-    int N, int K, float alpha, float beta, int tiles_m, int tiles_n) {
+    int N, int K, float alpha, float beta, int tiles_m, int tiles_n, EpiArgs epi) {
   constexpr int BK = 32;
   constexpr int WGM = kMfmaWaveRows<BM>, WGN = kMfmaWaveCols<BN>;
   constexpr int WPG = WGM * WGN;        // waves per group
@@ -965,7 +1104,7 @@ __global__ __launch_bounds__((kDmaThreads<BM, BN, KS>), 1) void gemm_mfma_dma_ke
           for (int r = 0; r < 16; ++r) acc[i][j][r] += smem[slot(g, i, j, r)];
   }
 
-  mfma_store_c_whole<MT, NT>(acc, C, N, m0, n0, wm, wn, h, c, alpha, beta);
+  mfma_epilogue<MT, NT, true, true, FUSED>(acc, C, M, N, m0, n0, wm, wn, h, c, alpha, beta, epi);
 }
 
 }  // namespace mcke_amd

@@ -265,6 +265,33 @@ def test_gemm_rejections(cpu_only):
     assert st.code == IA and "32-bit work size" in st.message
 
 
+def test_gemm_bias_act_rejections(cpu_only):
+    """The fused GEMM + bias + activation entry point: launch_gemm_f32's kMfmaF32
+    validation plus the bias, the activation and the output's aliasing."""
+    m = cpu_only
+    IA = m.StatusCode.kInvalidArgument
+    T = m.GemmTile
+    good = m.MFMA_TILES[0]
+    f = m.launch_gemm_bias_act_f32
+    assert f(X, B, W, Y, 0, 8, 8, 1, 3, good).ok()                  # empty: no launch
+    assert f(None, None, None, None, 8, 0, 8, 1, 3, good).ok()
+    assert f(X, B, None, Y, 8, 8, 8, 1, 3, good).code == IA         # null bias
+    assert f(X, None, W, Y, 8, 8, 8, 1, 3, good).code == IA         # null b
+    assert f(X, B, W, None, 8, 8, 8, 1, 3, good).code == IA         # null y
+    for out in (X, B, W):                                           # y aliases an input
+        assert f(X, B, W, out, 8, 8, 8, 1, 3, good).code == IA
+    assert f(X, B, W, Y, -8, 8, 8, 1, 3, good).code == IA
+    assert f(X, B, W, Y, 8, 8, -1, 1, 3, good).code == IA
+    assert f(X, B, W, Y, 8, 8, 1 << 31, 1, 3, good).code == IA
+    st = f(X, B, W, Y, 8, 8, 8, 1, 4, good)                         # bad activation
+    assert st.code == IA and "Activation" in st.message
+    assert f(X, B, W, Y, 8, 8, 8, 1, -1, good).code == IA
+    st = f(X, B, W, Y, 8, 8, 8, 1, 3, T(128, 128, 8, 8, 8))         # not a kMfmaF32 tile
+    assert st.code == IA and "no fallback" in st.message
+    st = f(X, B, W, Y, 1 << 17, 1 << 17, 8, 1, 3, T(32, 32, 32, 2, 2))
+    assert st.code == IA and "32-bit work size" in st.message
+
+
 def test_default_lp_tile(mcke):
     assert mcke.gemm_lp_default_tile(8192, 8192, 8192).astuple() == (256, 256, 64, 16, 16)
     assert mcke.gemm_lp_default_tile(4096, 4096, 4096).astuple() == (256, 256, 64, 16, 16)
