@@ -1081,6 +1081,63 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
     log(f"config 5 MLP: numerics gate {'PASS' if gate.passed else 'FAIL'}, timed plan same "
         f"bits: {same_bits}")
 
+    # The same block with each GEMM -> bias+act pair fused into the GEMM's epilogue
+    # (GemmBiasAct nodes): C never goes to memory and two launches go.  Same plan
+    # settings; its H, Z and Y must carry the unfused per-tensor plan's bits.
+    def mlp_fused_executor(**kw):
+        g, t = G.mlp_block_fused(T, D, F)
+        ex = G.Executor(g, **kw)
+        ex.plan()
+        for k, v in mlp_in.items():
+            ex.set_input(t[k], v)
+        return ex, t
+
+    # Fused and unfused timed in alternating blocks (their difference, about 1%, is
+    # below the run-to-run spread of two separate measurements).
+    ex, t = mlp_fused_executor(allocator=G.AllocatorKind.kBuddy,
+                               schedule=G.SchedulePolicy.kChainGreedy,
+                               memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4)
+    ex_u, _ = mlp_executor(False)
+    blocks_f, blocks_u, enq_fs = [], [], []
+    for _ in range(4):
+        w, e = timed_runs(ex, steps)
+        blocks_f.append(w)
+        enq_fs.append(e)
+        blocks_u.append(timed_runs(ex_u, steps)[0])
+    ex_u.close()
+    wall_f, enq_f = float(np.median(blocks_f)), float(np.median(enq_fs))
+    wall_u_alt = float(np.median(blocks_u))
+    y_fused_timed = ex.read(t["y"], T * D)
+    info_f = ex.plan_info()
+    ex.close()
+    ex, t = mlp_fused_executor(profile=True, profile_slots=warmup + steps, num_streams=4)
+    timed_runs(ex, steps)
+    timings_f = ex.timings()
+    ex.close()
+    ex, t = mlp_fused_executor(schedule=G.SchedulePolicy.kSequential,
+                               memory=G.MemoryPolicy.kAllocPerTensor, num_streams=1)
+    ex.run_sync()
+    fused_same = {k: bool(np.array_equal(ex.read(t[k], T * (F if k == "h" else D)).view(np.uint32),
+                                         host["mlp"][k].view(np.uint32))) for k in ("h", "z", "y")}
+    ex.close()
+    fused_same["y_timed_plan"] = bool(np.array_equal(y_fused_timed.view(np.uint32),
+                                                     host["mlp"]["y"].view(np.uint32)))
+    del y_fused_timed
+    out["mlp_block_fused"] = {
+        "shape": out["mlp_block"]["shape"], "nodes_in_graph": info_f["num_nodes"],
+        "wall_ms": round(wall_f, 4), "enqueue_us": round(enq_f, 2),
+        "tflops": round(info_f["total_flops"] / (wall_f * 1e-3) / 1e12, 2),
+        "unfused_wall_ms_alternating": round(wall_u_alt, 4),
+        "speedup_over_unfused": round(wall_u_alt / wall_f, 4),
+        "blocks": f"4 alternating blocks of {steps} runs each, fused then unfused; medians",
+        "nodes": [{"name": x["name"], "median_ms": round(x["median_ms"], 4)} for x in timings_f],
+        "arena_bytes": info_f["arena_bytes"],
+        "parity": {"ok": all(fused_same.values()), "same_bits_as_unfused": fused_same},
+    }
+    log(f"config 5 MLP, fused epilogues: {wall_f:.3f} ms/run against {wall_u_alt:.3f} unfused "
+        f"in alternating blocks ({wall_u_alt / wall_f:.3f}x), "
+        f"{out['mlp_block_fused']['tflops']} TFLOP/s, bits as unfused: {fused_same}")
+
     n, B, Dp = 2048, 4, 4
     fan_n = n
     fan_w = m.fill_random(n * n, 0x4000, -0.03125, 0.03125)
@@ -1557,6 +1614,10 @@ def headline(detail: dict, detail_file: str | None) -> dict:
         g = graph["mlp_block"]
         extra["graph_mlp"] = {"wall_ms": g.get("wall_ms"), "tflops": g.get("tflops"),
                               "bound_over_wall": g.get("bound_over_wall")}
+        fused = graph.get("mlp_block_fused")
+        if fused:
+            extra["graph_mlp"].update(fused_wall_ms=fused.get("wall_ms"),
+                                      fused_tflops=fused.get("tflops"))
     if graph.get("gates_passed") is not None:
         extra["graph_gates_passed"] = graph["gates_passed"]
     if graph.get("capture_choice"):
@@ -1611,7 +1672,7 @@ def main(argv=None) -> int:
                    help="skip the variant ladder (every variant the reference's benches time)")
     p.add_argument("--only", default=None,
                    help="comma-separated op-name prefixes to run (profiling); enables "
-                        "the copy_256mib calibration op")
+                        "the copy_256mib calibration op; 'graph' keeps the graph section")
     p.add_argument("--detail-out", default=os.path.join(ROOT, "gpurun_out", "bench_detail.json"),
                    help="file that receives the full record (every section); stdout's last "
                         "line carries the compact headline")
@@ -1642,7 +1703,7 @@ def main(argv=None) -> int:
     stream = m.Stream()
     ops, keep, gemm_bufs = build_ops(m, stream, only)
 
-    if only is not None and not ops and not any(x.startswith(("gemm_lp", "gemm_sweep")) for x in only):
+    if only is not None and not ops and not any(x.startswith(("gemm_lp", "gemm_sweep", "graph")) for x in only):
         print(f"bench.py: --only {args.only} names no op", file=sys.stderr)
         return 2
     log(f"warmup: {args.warmup} steps")
@@ -1684,7 +1745,7 @@ def main(argv=None) -> int:
             m, stream, with_peak=not args.no_peaks,
             vendor_sizes=tuple(int(x) for x in args.lp_vendor_sizes.split(",") if x))
     graph_res, graph_verify = None, None
-    if not (args.no_graph or only is not None):
+    if not (args.no_graph or (only is not None and "graph" not in only)):
         graph_res, graph_verify = graph_section(m)
     ladder_res, ladder_verify = None, None
     if not (args.no_ladder or only is not None):

@@ -110,6 +110,33 @@ class BiasActOp final : public Op {
   BiasActParams p_;
 };
 
+// GEMM with the bias + activation in its epilogue (no reference counterpart: the
+// reference chains GemmOp and BiasActOp).  Inputs A [m,k], B [k,n] and bias [n],
+// all fp32; y = act(alpha * A B + bias[col]) through
+// kernels::launch_gemm_bias_act_f32 (kMfmaF32), with the bits of the GemmOp ->
+// BiasActOp pair it replaces.  C never reaches memory, so the op costs the pair's
+// flops and the GEMM's bytes plus the bias.
+struct GemmBiasActParams {
+  float alpha = 1.f;
+  BiasActParams::Act act = BiasActParams::Act::kGeluTanh;
+  kernels::GemmTile tile{};
+  bool auto_tile = true;    // pick the kMfmaF32 tile per shape at launch
+};
+
+class GemmBiasActOp final : public Op {
+ public:
+  explicit GemmBiasActOp(GemmBiasActParams p) : p_(p) {}
+  [[nodiscard]] std::string_view type_name() const override { return "GemmBiasAct"; }
+  [[nodiscard]] Status launch(const OpContext&, const std::vector<Tensor>&,
+                              const std::vector<Tensor>&) override;
+  [[nodiscard]] StatusOr<std::vector<Shape>> infer_shapes(const std::vector<Shape>&) const override;
+  [[nodiscard]] OpCost cost(const std::vector<Shape>&) const override;
+  [[nodiscard]] const GemmBiasActParams& params() const noexcept { return p_; }
+
+ private:
+  GemmBiasActParams p_;
+};
+
 struct ReduceParams {
   enum class Kind { kSum, kMax, kMean } kind = Kind::kSum;
   int axis = -1;

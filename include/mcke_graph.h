@@ -111,6 +111,13 @@ int mcke_graph_add_bias_act(mcke_graph* g, uint32_t x, uint32_t bias, int act, i
 int mcke_graph_add_bias_act_rows(mcke_graph* g, uint32_t x, uint32_t bias, int act,
                                  int vector_width, int max_row_blocks, const char* name,
                                  uint32_t* out_tensor);
+/* No reference counterpart: GemmOp (kMfmaF32, beta = 0) and BiasActOp fused into one
+ * node, y = act(alpha * A B + bias[col]) through mcke_launch_gemm_bias_act_f32 --
+ * the bits of the GemmOp -> BiasActOp pair, without C.  NULL tile = per-shape
+ * choice. */
+int mcke_graph_add_gemm_bias_act(mcke_graph* g, uint32_t a, uint32_t b, uint32_t bias, float alpha,
+                                 int act, const mcke_gemm_tile* tile, const char* name,
+                                 uint32_t* out_tensor);
 int mcke_graph_add_reduce(mcke_graph* g, uint32_t x, int kind, int variant, const char* name,
                           uint32_t* out_tensor);
 int mcke_graph_add_softmax(mcke_graph* g, uint32_t x, int variant, const char* name, uint32_t* out_tensor);

@@ -96,6 +96,8 @@ def host_lib() -> C.CDLL:
                                              C.POINTER(GemmTile), C.c_char_p, _U32P]),
         "mcke_graph_add_gemm": (C.c_int, [_VP, _U32, _U32, C.c_float, C.c_int, C.POINTER(GemmTile),
                                           C.c_char_p, _U32P]),
+        "mcke_graph_add_gemm_bias_act": (C.c_int, [_VP, _U32, _U32, _U32, C.c_float, C.c_int,
+                                                   C.POINTER(GemmTile), C.c_char_p, _U32P]),
         "mcke_graph_add_bias_act": (C.c_int, [_VP, _U32, _U32, C.c_int, C.c_int, C.c_char_p, _U32P]),
         "mcke_graph_add_bias_act_rows": (C.c_int, [_VP, _U32, _U32, C.c_int, C.c_int, C.c_int,
                                                    C.c_char_p, _U32P]),
@@ -186,6 +188,15 @@ class Graph:
         tp = C.byref(tile) if tile is not None else None
         return self._out(host_lib().mcke_graph_add_gemm(self.h, a, b, alpha, int(variant), tp,
                                                         name.encode(), C.byref(out)), out)
+
+    def add_gemm_bias_act(self, a: int, b: int, bias: int, name: str, act=3,
+                          tile: GemmTile | None = None, alpha: float = 1.0) -> int:
+        """GEMM (kMfmaF32) with the bias + activation in its epilogue: one node with
+        the bits of add_gemm -> add_bias_act.  tile None: the per-shape default."""
+        out = C.c_uint32()
+        tp = C.byref(tile) if tile is not None else None
+        return self._out(host_lib().mcke_graph_add_gemm_bias_act(
+            self.h, a, b, bias, alpha, int(act), tp, name.encode(), C.byref(out)), out)
 
     def add_bias_act(self, x: int, bias: int, name: str, act=3, vector_width: int = 0,
                      max_row_blocks: int = 0) -> int:
@@ -349,6 +360,24 @@ def mlp_block(tokens: int, d_model: int, d_ff: int, gemm_variant=GemmVariant.kMf
     g.mark_output(y)
     return g, {"x": x, "W1": w1, "b1": b1, "W2": w2, "b2": b2, "gemm1": g1, "h": h, "gemm2": g2,
                "z": z, "y": y}
+
+
+def mlp_block_fused(tokens: int, d_model: int, d_ff: int):
+    """mlp_block with each GEMM -> bias+act pair as one fused node:
+    H = GELU(X W1 + b1) and Z = H W2 + b2 in the GEMMs' epilogues, then softmax(Z).
+    The same tensors under the same names (no "gemm1"/"gemm2": C is never stored),
+    and the same output bits."""
+    g = Graph()
+    x = g.add_input((tokens, d_model), "x")
+    w1 = g.add_input((d_model, d_ff), "W1")
+    b1 = g.add_input((d_ff,), "b1")
+    w2 = g.add_input((d_ff, d_model), "W2")
+    b2 = g.add_input((d_model,), "b2")
+    h = g.add_gemm_bias_act(x, w1, b1, "gemm1_bias_gelu", act=3)
+    z = g.add_gemm_bias_act(h, w2, b2, "gemm2_bias_add", act=0)
+    y = g.add_softmax(z, "softmax")
+    g.mark_output(y)
+    return g, {"x": x, "W1": w1, "b1": b1, "W2": w2, "b2": b2, "h": h, "z": z, "y": y}
 
 
 def gemm_fanout(branches: int, depth: int, n: int, gemm_variant=GemmVariant.kMfmaF32):

@@ -106,6 +106,21 @@ int mcke_graph_add_gemm(mcke_graph* g, uint32_t a, uint32_t b, float alpha, int 
   return add_op<mcke::GemmOp>(g, std::make_unique<mcke::GemmOp>(p), {a, b}, name, out);
 }
 
+int mcke_graph_add_gemm_bias_act(mcke_graph* g, uint32_t a, uint32_t b, uint32_t bias, float alpha,
+                                 int act, const mcke_gemm_tile* tile, const char* name,
+                                 uint32_t* out) {
+  if (act < 0 || act > 3) return bad("mcke_graph_add_gemm_bias_act: unknown activation");
+  mcke::GemmBiasActParams p;
+  p.alpha = alpha;
+  p.act = static_cast<mcke::BiasActParams::Act>(act);
+  if (tile) {
+    p.tile = mcke::kernels::GemmTile{tile->bm, tile->bn, tile->bk, tile->tm, tile->tn};
+    p.auto_tile = false;
+  }
+  return add_op<mcke::GemmBiasActOp>(g, std::make_unique<mcke::GemmBiasActOp>(p), {a, b, bias},
+                                     name, out);
+}
+
 int mcke_graph_add_bias_act_rows(mcke_graph* g, uint32_t x, uint32_t bias, int act,
                                  int vector_width, int max_row_blocks, const char* name,
                                  uint32_t* out) {

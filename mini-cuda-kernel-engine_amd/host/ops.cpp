@@ -191,6 +191,56 @@ Status BiasActOp::launch(const OpContext& ctx, const std::vector<Tensor>& inputs
 }
 
 // ---------------------------------------------------------------------------
+StatusOr<std::vector<Shape>> GemmBiasActOp::infer_shapes(const std::vector<Shape>& in) const {
+  if (in.size() != 3)
+    return InvalidArgumentError("GemmBiasActOp: expects 3 inputs (A, B, bias), got " +
+                                std::to_string(in.size()));
+  if (in[0].rank() != 2 || in[1].rank() != 2 || in[2].rank() != 1)
+    return InvalidArgumentError("GemmBiasActOp: A and B must be rank 2 and the bias rank 1");
+  const dim_t m = in[0].dim(0), k = in[0].dim(1), k2 = in[1].dim(0), n = in[1].dim(1);
+  if (k != k2)
+    return InvalidArgumentError("GemmBiasActOp: inner dimensions disagree: A is [" +
+                                std::to_string(m) + "," + std::to_string(k) + "], B is [" +
+                                std::to_string(k2) + "," + std::to_string(n) + "]");
+  if (in[2].dim(0) != n)
+    return InvalidArgumentError("GemmBiasActOp: bias length " + std::to_string(in[2].dim(0)) +
+                                " does not match B's columns " + std::to_string(n));
+  if (!p_.auto_tile && !kernels::gemm_tile_is_supported(kernels::GemmVariant::kMfmaF32, p_.tile))
+    return InvalidArgumentError("GemmBiasActOp: tile " + tile_str(p_.tile) +
+                                " is not a kMfmaF32 tile ((256,256,32|16,16,16), "
+                                "(128,128,32|16,8,8), (64,64,32,4,4), (32,32,32,2,2))");
+  return std::vector<Shape>{Shape{m, n}};
+}
+
+OpCost GemmBiasActOp::cost(const std::vector<Shape>& in) const {
+  OpCost c;
+  if (in.size() != 3 || in[0].rank() != 2 || in[1].rank() != 2) return c;
+  const auto m = static_cast<std::uint64_t>(in[0].dim(0));
+  const auto k = static_cast<std::uint64_t>(in[0].dim(1));
+  const auto n = static_cast<std::uint64_t>(in[1].dim(1));
+  c.flops = 2ull * m * n * k + m * n * act_flops_per_elem(p_.act);
+  c.bytes = (m * k + k * n + n + m * n) * sizeof(float);
+  return c;
+}
+
+Status GemmBiasActOp::launch(const OpContext& ctx, const std::vector<Tensor>& inputs,
+                             const std::vector<Tensor>& outputs) {
+  if (inputs.size() != 3 || outputs.size() != 1)
+    return InvalidArgumentError("GemmBiasActOp::launch: expects 3 inputs and 1 output");
+  const float* a = inputs[0].data_as<float>();
+  const float* b = inputs[1].data_as<float>();
+  const float* bias = inputs[2].data_as<float>();
+  float* y = outputs[0].data_as<float>();
+  if (!a || !b || !bias || !y)
+    return InvalidArgumentError("GemmBiasActOp::launch: a tensor is undefined or not f32");
+  const dim_t m = inputs[0].shape().dim(0), k = inputs[0].shape().dim(1), n = inputs[1].shape().dim(1);
+  const kernels::GemmTile tile = p_.auto_tile ? kernels::mfma_default_tile(m, n, k) : p_.tile;
+  return kernels::launch_gemm_bias_act_f32(a, b, bias, y, m, n, k, p_.alpha,
+                                           static_cast<kernels::Activation>(p_.act), tile,
+                                           ctx.stream);
+}
+
+// ---------------------------------------------------------------------------
 StatusOr<std::vector<Shape>> ReduceOp::infer_shapes(const std::vector<Shape>& in) const {
   if (in.size() != 1)
     return InvalidArgumentError("ReduceOp: expects 1 input, got " + std::to_string(in.size()));

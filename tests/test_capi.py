@@ -74,6 +74,29 @@ def test_graph_builder_without_gpu(mcke):
         g2.add_gemm(x, x, "tiled_no_tile", variant=mcke.GemmVariant.kTiledSmem)
 
 
+def test_fused_gemm_node_without_gpu(mcke):
+    """GemmBiasAct nodes: shapes, the checks at build time, and the fused MLP's
+    tensors matching the unfused one's."""
+    from mcke_amd import graph
+    g, t = graph.mlp_block_fused(64, 32, 128)
+    assert g.shape(t["h"]) == (64, 128) and g.shape(t["z"]) == (64, 32)
+    assert g.shape(t["y"]) == (64, 32)
+    g2 = graph.Graph()
+    a = g2.add_input((8, 16), "a")
+    b = g2.add_input((16, 12), "b")
+    ok_bias, bad_bias = g2.add_input((12,), "bias"), g2.add_input((16,), "bias16")
+    assert g2.shape(g2.add_gemm_bias_act(a, b, ok_bias, "y")) == (8, 12)
+    IA = mcke.StatusCode.kInvalidArgument
+    for args in ((a, b, bad_bias), (a, a, ok_bias), (b, b, ok_bias)):
+        with pytest.raises(mcke.MckeError) as ei:
+            g2.add_gemm_bias_act(*args, "bad")
+        assert ei.value.status.code == IA
+    with pytest.raises(mcke.MckeError):                       # not a kMfmaF32 tile
+        g2.add_gemm_bias_act(a, b, ok_bias, "bad_tile", tile=mcke.GemmTile(128, 128, 8, 8, 8))
+    with pytest.raises(mcke.MckeError):                       # unknown activation
+        g2.add_gemm_bias_act(a, b, ok_bias, "bad_act", act=7)
+
+
 def test_graph_dtypes_without_gpu(mcke):
     """16-bit inputs: only GEMM nodes take them; the output dtype follows the op."""
     from mcke_amd import graph

@@ -88,6 +88,55 @@ def test_mlp_block_same_bits_under_every_plan(G, orc, schedule, memory):
     assert np.array_equal(gold.view(np.uint32), got.view(np.uint32))
 
 
+@pytest.mark.parametrize("shape", [(256, 128, 512), (200, 96, 320)], ids=["whole", "ragged"])
+def test_fused_mlp_block_has_the_unfused_bits(G, orc, shape):
+    """mlp_block_fused (GemmBiasAct nodes: bias+GELU and the bias add in the GEMMs'
+    epilogues) against mlp_block: H, Z and Y bit for bit, on a per-tensor plan and on
+    a 4-stream chain-greedy plan with arena reuse over poisoned buffers; the fused
+    graph has 3 nodes, and the numerics gate passes on it."""
+    T, D, F = shape
+    inp = _mlp_inputs(orc, T, D, F)
+
+    def run(build, names, **kw):
+        g, t = build(T, D, F)
+        ex = G.Executor(g, **kw)
+        ex.plan()
+        for k, v in inp.items():
+            ex.set_input(t[k], v)
+        ex.run_sync()
+        ex.run_sync()
+        sizes = {"h": T * F, "z": T * D, "y": T * D}
+        outs = {k: ex.read(t[k], sizes[k]) for k in names}
+        info = ex.plan_info()
+        ex.close()
+        return outs, info
+
+    per_tensor = dict(schedule=G.SchedulePolicy.kSequential, memory=G.MemoryPolicy.kAllocPerTensor,
+                      num_streams=1)
+    gold, _ = run(G.mlp_block, ("h", "z", "y"), **per_tensor)
+    fused, info = run(G.mlp_block_fused, ("h", "z", "y"), **per_tensor)
+    assert info["num_nodes"] == 3
+    for k in ("h", "z", "y"):
+        assert np.array_equal(gold[k].view(np.uint32), fused[k].view(np.uint32)), k
+    reuse, _ = run(G.mlp_block_fused, ("y",), schedule=G.SchedulePolicy.kChainGreedy,
+                   memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4, poison_buffers=True)
+    assert np.array_equal(gold["y"].view(np.uint32), reuse["y"].view(np.uint32))
+    # And against the oracle chain from the original inputs.
+    r1 = orc.gemm(inp["x"], inp["W1"], np.zeros(T * F, np.float32), T, F, D)
+    r2 = orc.gemm(orc.bias_act(r1, inp["b1"], T, F, 3), inp["W2"], np.zeros(T * D, np.float32),
+                  T, D, F)
+    ref = orc.row_softmax(orc.bias_act(r2, inp["b2"], T, D, 0), T, D)
+    assert np.max(np.abs(fused["y"] - ref)) < 1e-5
+    g, t = G.mlp_block_fused(T, D, F)
+    ex = G.Executor(g, num_streams=4, validate_numerics=True)
+    ex.plan()
+    for k, v in inp.items():
+        ex.set_input(t[k], v)
+    res = ex.validate_numerics(repeats=3)
+    ex.close()
+    assert res.passed and res.configs_compared == 9, res.detail
+
+
 def test_numerics_gate_passes(G, orc):
     T, D, F = 128, 64, 256
     g, t = G.mlp_block(T, D, F)
