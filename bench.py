@@ -953,7 +953,7 @@ def gemm_lp_section(m, stream, iters=10, with_peak=True, vendor_sizes=(8192, 409
     return out, verifies
 
 
-def graph_section(m, steps=5, warmup=2, gate_repeats=20):
+def graph_section(m, steps=5, warmup=2, gate_repeats=20, capture=True):
     """BASELINE config 5 through the GraphExecutor (buddy allocator, chain-greedy
     schedule, happens-before arena reuse):
       * the MLP block X[4096x4096] -> GEMM(W1 4096x16384) -> bias+GELU -> GEMM(W2)
@@ -1267,138 +1267,141 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20):
             + f"; numerics gate {'PASS' if gate.passed else 'FAIL'}")
     out["reference_graphs"] = ref_graphs
 
-    # Launch-bound shapes: the same MLP chain at small sizes, replayed eagerly (the
-    # plan's launches issued by the host each run) and as one captured HIP graph
-    # launch per run.
-    out["mlp_small_capture"] = []
-    for (T2, D2, F2) in ((512, 256, 1024), (64, 64, 256)):
-        cap = {}
+    # The HIP-graph capture part (skipped with capture=False: under rocprofv3's kernel
+    # trace the host process crashed inside it, so profiling runs leave it out).
+    if capture:
+        # Launch-bound shapes: the same MLP chain at small sizes, replayed eagerly (the
+        # plan's launches issued by the host each run) and as one captured HIP graph
+        # launch per run.
+        out["mlp_small_capture"] = []
+        for (T2, D2, F2) in ((512, 256, 1024), (64, 64, 256)):
+            cap = {}
+            for label in ("eager", "hip_graph"):
+                g, t = G.mlp_block(T2, D2, F2)
+                ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList,
+                                schedule=G.SchedulePolicy.kChainGreedy,
+                                memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=2)
+                ex.plan()
+                ex.set_input(t["x"], m.fill_normal(T2 * D2, 0x3101, 0.0, 1.0))
+                ex.set_input(t["W1"], m.fill_normal(D2 * F2, 0x3102, 0.0, 0.02))
+                ex.set_input(t["b1"], m.fill_normal(F2, 0x3103, 0.0, 0.01))
+                ex.set_input(t["W2"], m.fill_normal(F2 * D2, 0x3104, 0.0, 0.02))
+                ex.set_input(t["b2"], m.fill_normal(D2, 0x3105, 0.0, 0.01))
+                if label == "hip_graph":
+                    ex.capture()
+                wall, _ = timed_runs(ex, 200)
+                y = ex.read(t["y"], T2 * D2)
+                cap[label] = {"us_per_run": round(wall * 1e3, 2), "y_bits": y.view(np.uint32)}
+                ex.close()
+            same = bool(np.array_equal(cap["eager"].pop("y_bits"), cap["hip_graph"].pop("y_bits")))
+            entry = {"shape": f"X[{T2}x{D2}] W1[{D2}x{F2}] W2[{F2}x{D2}]", **cap,
+                     "speedup": round(cap["eager"]["us_per_run"] / cap["hip_graph"]["us_per_run"], 3),
+                     "same_bits": same}
+            log(f"MLP {T2}x{D2}x{F2}: eager {cap['eager']['us_per_run']} us, "
+                f"hipGraph {cap['hip_graph']['us_per_run']} us per run, same bits: {same}")
+            out["mlp_small_capture"].append(entry)
+
+        # A launch-bound plan, on 4 streams and on one: eager (the host issues the
+        # launches, events and waits each run) vs one captured graph per run (on 4
+        # streams assembled node by node from single-stream captures).
+        n, B, Dp = 256, 4, 4
+        fan_cap = {"shape": f"{B} chains x {Dp} GEMMs {n}^3"}
+        bits_seen = []
+        for plan_label, sched, streams in (("4_streams", G.SchedulePolicy.kChainGreedy, 4),
+                                           ("1_stream", G.SchedulePolicy.kSequential, 1)):
+            cap = {}
+            for label in ("eager", "hip_graph"):
+                g, t = G.gemm_fanout(B, Dp, n)
+                ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList, schedule=sched,
+                                memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=streams)
+                ex.plan()
+                ex.set_input(t["W"], m.fill_random(n * n, 0x4100, -0.0625, 0.0625))
+                for k in range(B):
+                    ex.set_input(t["xs"][k], m.fill_random(n * n, 0x4101 + k))
+                if label == "hip_graph":
+                    ex.capture()
+                wall, _ = timed_runs(ex, 200)
+                bits_seen.append(np.concatenate([ex.read(o, n * n).view(np.uint32) for o in t["outs"]]))
+                cap[label] = {"us_per_run": round(wall * 1e3, 2)}
+                ex.close()
+            cap["speedup"] = round(cap["eager"]["us_per_run"] / cap["hip_graph"]["us_per_run"], 3)
+            fan_cap[plan_label] = cap
+            log(f"fan-out {B}x{Dp} {n}^3 {plan_label}: eager {cap['eager']['us_per_run']} us, "
+                f"hipGraph {cap['hip_graph']['us_per_run']} us per run")
+        fan_cap["same_bits"] = all(np.array_equal(bits_seen[0], b) for b in bits_seen[1:])
+        out["fanout_small_capture"] = fan_cap
+
+        # A plan of many short nodes, where one graph launch replaces many eager ones: a
+        # chain of 32 bias+GELU nodes over X[64 x 1024] (256 KiB, about a microsecond
+        # of device work each) on one stream, eager vs replayed.
+        chain_cap = {"shape": "chain of 32 bias+GELU nodes, X[64x1024], 1 stream"}
+        chain_bits = []
         for label in ("eager", "hip_graph"):
-            g, t = G.mlp_block(T2, D2, F2)
+            g, t = G.chain(32, 64, 1024)
             ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList,
-                            schedule=G.SchedulePolicy.kChainGreedy,
-                            memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=2)
+                            schedule=G.SchedulePolicy.kSequential,
+                            memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=1)
             ex.plan()
-            ex.set_input(t["x"], m.fill_normal(T2 * D2, 0x3101, 0.0, 1.0))
-            ex.set_input(t["W1"], m.fill_normal(D2 * F2, 0x3102, 0.0, 0.02))
-            ex.set_input(t["b1"], m.fill_normal(F2, 0x3103, 0.0, 0.01))
-            ex.set_input(t["W2"], m.fill_normal(F2 * D2, 0x3104, 0.0, 0.02))
-            ex.set_input(t["b2"], m.fill_normal(D2, 0x3105, 0.0, 0.01))
+            ex.set_input(t["x"], m.fill_normal(64 * 1024, 0x5100))
+            ex.set_input(t["bias"], m.fill_random(1024, 0x5101, -0.5, 0.5))
             if label == "hip_graph":
                 ex.capture()
-            wall, _ = timed_runs(ex, 200)
-            y = ex.read(t["y"], T2 * D2)
-            cap[label] = {"us_per_run": round(wall * 1e3, 2), "y_bits": y.view(np.uint32)}
+            wall, enq = timed_runs(ex, 200)
+            chain_bits.append(ex.read(t["outs"][0], 64 * 1024).view(np.uint32))
+            chain_cap[label] = {"us_per_run": round(wall * 1e3, 2), "enqueue_us": round(enq, 2)}
             ex.close()
-        same = bool(np.array_equal(cap["eager"].pop("y_bits"), cap["hip_graph"].pop("y_bits")))
-        entry = {"shape": f"X[{T2}x{D2}] W1[{D2}x{F2}] W2[{F2}x{D2}]", **cap,
-                 "speedup": round(cap["eager"]["us_per_run"] / cap["hip_graph"]["us_per_run"], 3),
-                 "same_bits": same}
-        log(f"MLP {T2}x{D2}x{F2}: eager {cap['eager']['us_per_run']} us, "
-            f"hipGraph {cap['hip_graph']['us_per_run']} us per run, same bits: {same}")
-        out["mlp_small_capture"].append(entry)
+        chain_cap["speedup"] = round(chain_cap["eager"]["us_per_run"] /
+                                     chain_cap["hip_graph"]["us_per_run"], 3)
+        chain_cap["same_bits"] = bool(np.array_equal(chain_bits[0], chain_bits[1]))
+        out["chain32_small_capture"] = chain_cap
+        log(f"chain32 64x1024: eager {chain_cap['eager']['us_per_run']} us, hipGraph "
+            f"{chain_cap['hip_graph']['us_per_run']} us per run")
 
-    # A launch-bound plan, on 4 streams and on one: eager (the host issues the
-    # launches, events and waits each run) vs one captured graph per run (on 4
-    # streams assembled node by node from single-stream captures).
-    n, B, Dp = 256, 4, 4
-    fan_cap = {"shape": f"{B} chains x {Dp} GEMMs {n}^3"}
-    bits_seen = []
-    for plan_label, sched, streams in (("4_streams", G.SchedulePolicy.kChainGreedy, 4),
-                                       ("1_stream", G.SchedulePolicy.kSequential, 1)):
-        cap = {}
-        for label in ("eager", "hip_graph"):
-            g, t = G.gemm_fanout(B, Dp, n)
-            ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList, schedule=sched,
-                            memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=streams)
+        # The executor's measured choice (capture_if_faster) on each launch-bound plan:
+        # it keeps the graph only where replay beat eager issue on that plan.
+        def choice(build, set_inputs, **kw):
+            g, t = build()
+            ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList,
+                            memory=G.MemoryPolicy.kReuseHappensBefore, **kw)
             ex.plan()
-            ex.set_input(t["W"], m.fill_random(n * n, 0x4100, -0.0625, 0.0625))
-            for k in range(B):
-                ex.set_input(t["xs"][k], m.fill_random(n * n, 0x4101 + k))
-            if label == "hip_graph":
-                ex.capture()
-            wall, _ = timed_runs(ex, 200)
-            bits_seen.append(np.concatenate([ex.read(o, n * n).view(np.uint32) for o in t["outs"]]))
-            cap[label] = {"us_per_run": round(wall * 1e3, 2)}
+            set_inputs(ex, t)
+            d = ex.capture_if_faster(trials=100)
             ex.close()
-        cap["speedup"] = round(cap["eager"]["us_per_run"] / cap["hip_graph"]["us_per_run"], 3)
-        fan_cap[plan_label] = cap
-        log(f"fan-out {B}x{Dp} {n}^3 {plan_label}: eager {cap['eager']['us_per_run']} us, "
-            f"hipGraph {cap['hip_graph']['us_per_run']} us per run")
-    fan_cap["same_bits"] = all(np.array_equal(bits_seen[0], b) for b in bits_seen[1:])
-    out["fanout_small_capture"] = fan_cap
+            return {k: (round(v, 2) if isinstance(v, float) else v) for k, v in d.items()}
 
-    # A plan of many short nodes, where one graph launch replaces many eager ones: a
-    # chain of 32 bias+GELU nodes over X[64 x 1024] (256 KiB, about a microsecond
-    # of device work each) on one stream, eager vs replayed.
-    chain_cap = {"shape": "chain of 32 bias+GELU nodes, X[64x1024], 1 stream"}
-    chain_bits = []
-    for label in ("eager", "hip_graph"):
-        g, t = G.chain(32, 64, 1024)
-        ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList,
-                        schedule=G.SchedulePolicy.kSequential,
-                        memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=1)
-        ex.plan()
-        ex.set_input(t["x"], m.fill_normal(64 * 1024, 0x5100))
-        ex.set_input(t["bias"], m.fill_random(1024, 0x5101, -0.5, 0.5))
-        if label == "hip_graph":
-            ex.capture()
-        wall, enq = timed_runs(ex, 200)
-        chain_bits.append(ex.read(t["outs"][0], 64 * 1024).view(np.uint32))
-        chain_cap[label] = {"us_per_run": round(wall * 1e3, 2), "enqueue_us": round(enq, 2)}
-        ex.close()
-    chain_cap["speedup"] = round(chain_cap["eager"]["us_per_run"] /
-                                 chain_cap["hip_graph"]["us_per_run"], 3)
-    chain_cap["same_bits"] = bool(np.array_equal(chain_bits[0], chain_bits[1]))
-    out["chain32_small_capture"] = chain_cap
-    log(f"chain32 64x1024: eager {chain_cap['eager']['us_per_run']} us, hipGraph "
-        f"{chain_cap['hip_graph']['us_per_run']} us per run")
+        def mlp_inputs_small(T2, D2, F2):
+            def f(ex, t):
+                ex.set_input(t["x"], m.fill_normal(T2 * D2, 0x3101, 0.0, 1.0))
+                ex.set_input(t["W1"], m.fill_normal(D2 * F2, 0x3102, 0.0, 0.02))
+                ex.set_input(t["b1"], m.fill_normal(F2, 0x3103, 0.0, 0.01))
+                ex.set_input(t["W2"], m.fill_normal(F2 * D2, 0x3104, 0.0, 0.02))
+                ex.set_input(t["b2"], m.fill_normal(D2, 0x3105, 0.0, 0.01))
+            return f
 
-    # The executor's measured choice (capture_if_faster) on each launch-bound plan:
-    # it keeps the graph only where replay beat eager issue on that plan.
-    def choice(build, set_inputs, **kw):
-        g, t = build()
-        ex = G.Executor(g, allocator=G.AllocatorKind.kFreeList,
-                        memory=G.MemoryPolicy.kReuseHappensBefore, **kw)
-        ex.plan()
-        set_inputs(ex, t)
-        d = ex.capture_if_faster(trials=100)
-        ex.close()
-        return {k: (round(v, 2) if isinstance(v, float) else v) for k, v in d.items()}
+        def fan_inputs_small(ex, t):
+            ex.set_input(t["W"], m.fill_random(256 * 256, 0x4100, -0.0625, 0.0625))
+            for k, x in enumerate(t["xs"]):
+                ex.set_input(x, m.fill_random(256 * 256, 0x4101 + k))
 
-    def mlp_inputs_small(T2, D2, F2):
-        def f(ex, t):
-            ex.set_input(t["x"], m.fill_normal(T2 * D2, 0x3101, 0.0, 1.0))
-            ex.set_input(t["W1"], m.fill_normal(D2 * F2, 0x3102, 0.0, 0.02))
-            ex.set_input(t["b1"], m.fill_normal(F2, 0x3103, 0.0, 0.01))
-            ex.set_input(t["W2"], m.fill_normal(F2 * D2, 0x3104, 0.0, 0.02))
-            ex.set_input(t["b2"], m.fill_normal(D2, 0x3105, 0.0, 0.01))
-        return f
+        def chain_inputs(ex, t):
+            ex.set_input(t["x"], m.fill_normal(64 * 1024, 0x5100))
+            ex.set_input(t["bias"], m.fill_random(1024, 0x5101, -0.5, 0.5))
 
-    def fan_inputs_small(ex, t):
-        ex.set_input(t["W"], m.fill_random(256 * 256, 0x4100, -0.0625, 0.0625))
-        for k, x in enumerate(t["xs"]):
-            ex.set_input(x, m.fill_random(256 * 256, 0x4101 + k))
-
-    def chain_inputs(ex, t):
-        ex.set_input(t["x"], m.fill_normal(64 * 1024, 0x5100))
-        ex.set_input(t["bias"], m.fill_random(1024, 0x5101, -0.5, 0.5))
-
-    out["capture_choice"] = {
-        "mlp_512x256x1024_2streams": choice(lambda: G.mlp_block(512, 256, 1024),
-                                            mlp_inputs_small(512, 256, 1024),
-                                            schedule=G.SchedulePolicy.kChainGreedy, num_streams=2),
-        "mlp_64x64x256_2streams": choice(lambda: G.mlp_block(64, 64, 256),
-                                         mlp_inputs_small(64, 64, 256),
-                                         schedule=G.SchedulePolicy.kChainGreedy, num_streams=2),
-        "fanout_4x4_256_4streams": choice(lambda: G.gemm_fanout(4, 4, 256), fan_inputs_small,
-                                          schedule=G.SchedulePolicy.kChainGreedy, num_streams=4),
-        "chain32_64x1024_1stream": choice(lambda: G.chain(32, 64, 1024), chain_inputs,
-                                          schedule=G.SchedulePolicy.kSequential, num_streams=1),
-    }
-    for k, v in out["capture_choice"].items():
-        log(f"capture_if_faster {k}: eager {v['eager_us_per_run']} us, replay "
-            f"{v['replay_us_per_run']} us -> {'graph' if v['captured'] else 'eager'}")
+        out["capture_choice"] = {
+            "mlp_512x256x1024_2streams": choice(lambda: G.mlp_block(512, 256, 1024),
+                                                mlp_inputs_small(512, 256, 1024),
+                                                schedule=G.SchedulePolicy.kChainGreedy, num_streams=2),
+            "mlp_64x64x256_2streams": choice(lambda: G.mlp_block(64, 64, 256),
+                                             mlp_inputs_small(64, 64, 256),
+                                             schedule=G.SchedulePolicy.kChainGreedy, num_streams=2),
+            "fanout_4x4_256_4streams": choice(lambda: G.gemm_fanout(4, 4, 256), fan_inputs_small,
+                                              schedule=G.SchedulePolicy.kChainGreedy, num_streams=4),
+            "chain32_64x1024_1stream": choice(lambda: G.chain(32, 64, 1024), chain_inputs,
+                                              schedule=G.SchedulePolicy.kSequential, num_streams=1),
+        }
+        for k, v in out["capture_choice"].items():
+            log(f"capture_if_faster {k}: eager {v['eager_us_per_run']} us, replay "
+                f"{v['replay_us_per_run']} us -> {'graph' if v['captured'] else 'eager'}")
 
     out["gates_passed"] = bool(out["mlp_block"]["gate"]["passed"] and
                                out["fanout4x4_gemm2048"]["gate"]["passed"] and
@@ -1665,6 +1668,8 @@ def main(argv=None) -> int:
                    help="target CPU time of the GEMM slab's timed runs together")
     p.add_argument("--no-graph", action="store_true", help="skip the config-5 graph section")
     p.add_argument("--no-peaks", action="store_true", help="skip the measured-peak microbenches")
+    p.add_argument("--no-capture", action="store_true",
+                   help="skip the graph section's HIP-graph capture part (for profiling runs)")
     p.add_argument("--no-lp", action="store_true", help="skip the 16-bit-input GEMM section")
     p.add_argument("--lp-vendor-sizes", default="8192,4096,2048,1024",
                    help="sizes of the 16-bit GEMM's interleaved rocBLAS comparison")
@@ -1746,7 +1751,7 @@ def main(argv=None) -> int:
             vendor_sizes=tuple(int(x) for x in args.lp_vendor_sizes.split(",") if x))
     graph_res, graph_verify = None, None
     if not (args.no_graph or (only is not None and "graph" not in only)):
-        graph_res, graph_verify = graph_section(m)
+        graph_res, graph_verify = graph_section(m, capture=not args.no_capture)
     ladder_res, ladder_verify = None, None
     if not (args.no_ladder or only is not None):
         ladder_res, ladder_verify = ladder_section(m, stream, info.sm_count)
