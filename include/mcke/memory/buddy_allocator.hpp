@@ -33,7 +33,7 @@ namespace mcke {
 // requests above 4 GiB bypass the slabs.
 struct BuddyConfig {
   std::size_t initial_slab_bytes = std::size_t{1} << 30;
-  std::size_t max_total_bytes = 0;   // 0 = unlimited
+  std::size_t max_total_bytes = 0;   // cap on the slabs' bytes (0 = unlimited); bypass allocations do not count
   std::size_t min_block_bytes = kMinBlockBytes;
   double growth_factor = 2.0;
   std::size_t large_alloc_threshold = std::size_t{4} << 30;

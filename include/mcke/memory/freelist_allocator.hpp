@@ -40,7 +40,7 @@ namespace mcke {
 // powers of two up to 1 GiB, and only requests above 1 GiB bypass the slabs.
 struct FreeListConfig {
   std::size_t slab_bytes = std::size_t{1} << 30;
-  std::size_t max_total_bytes = 0;   // 0 = unlimited
+  std::size_t max_total_bytes = 0;   // cap on the slabs' bytes (0 = unlimited); bypass allocations do not count
   std::size_t small_class_granularity = 512;
   std::size_t small_large_split = std::size_t{1} << 20;
   std::size_t large_alloc_threshold = std::size_t{1} << 30;

@@ -68,10 +68,16 @@ StatusOr<std::uint32_t> BuddyAllocator::add_slab(std::size_t min_bytes) {
   want = std::max(want, min_bytes);
   std::size_t bytes = std::size_t{1} << log2_ceil(std::max(want, cfg_.min_block_bytes));
   if (cfg_.max_total_bytes) {
-    if (stats_.bytes_reserved + (std::size_t{1} << log2_ceil(min_bytes)) > cfg_.max_total_bytes)
+    // The cap bounds the pool's slabs; allocations that bypass the pool are the
+    // caller's own and do not count (reference buddy_allocator.cpp:185-195).
+    std::size_t in_slabs = 0;
+    for (const Slab& s : slabs_)
+      if (s.base) in_slabs += s.bytes;
+    if (in_slabs + (std::size_t{1} << log2_ceil(min_bytes)) > cfg_.max_total_bytes)
       return OutOfMemoryError("BuddyAllocator: max_total_bytes (" + std::to_string(cfg_.max_total_bytes) +
-                              ") would be exceeded");
-    while (bytes > min_bytes && stats_.bytes_reserved + bytes > cfg_.max_total_bytes) bytes >>= 1;
+                              ") would be exceeded by the pool's slabs (" + std::to_string(in_slabs) +
+                              " B reserved in slabs)");
+    while (bytes > min_bytes && in_slabs + bytes > cfg_.max_total_bytes) bytes >>= 1;
     if (bytes < min_bytes) bytes = std::size_t{1} << log2_ceil(min_bytes);
   }
   MCKE_ASSIGN_OR_RETURN(void* base, raw_alloc(bytes));

@@ -82,9 +82,15 @@ std::size_t FreeListAllocator::class_block_bytes(std::size_t cls) const {
 }
 
 StatusOr<std::uint32_t> FreeListAllocator::add_slab(std::size_t bytes) {
-  if (cfg_.max_total_bytes && stats_.bytes_reserved + bytes > cfg_.max_total_bytes)
+  // The cap bounds the pool's slabs; bypass allocations do not count (reference
+  // freelist_allocator.cpp:134-143).
+  std::size_t in_slabs = 0;
+  for (const Slab& s : slabs_)
+    if (s.base) in_slabs += s.bytes;
+  if (cfg_.max_total_bytes && in_slabs + bytes > cfg_.max_total_bytes)
     return OutOfMemoryError("FreeListAllocator: a slab of " + std::to_string(bytes) +
-                            " B would exceed max_total_bytes (" + std::to_string(cfg_.max_total_bytes) + ")");
+                            " B would exceed max_total_bytes (" + std::to_string(cfg_.max_total_bytes) +
+                            ") with " + std::to_string(in_slabs) + " B already in slabs");
   MCKE_ASSIGN_OR_RETURN(void* base, raw_alloc(bytes));
   ++stats_.raw_malloc_calls;
   stats_.bytes_reserved += bytes;

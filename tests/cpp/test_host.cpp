@@ -1096,6 +1096,49 @@ TEST(freelist_split_blocking_drain_and_oom) {
   CHECK_OK(f.validate());
 }
 
+// max_total_bytes caps the pools' slabs only: a bypass allocation larger than the
+// cap is the caller's own and does not stop the pool growing (the reference's
+// checks, buddy_allocator.cpp:185-195 and freelist_allocator.cpp:134-143; its
+// allocator bench's dl_transformer_bypass trace needs exactly this).
+TEST(max_total_bytes_caps_slabs_not_bypass) {
+  {
+    BuddyConfig cfg = small_cfg(ReusePolicy::kCoarseStreamPoll);
+    cfg.max_total_bytes = 3 << 20;                       // room for 1 MiB + 2 MiB of slabs
+    HostBuddy b(cfg);
+    const auto s1 = fake_stream(1);
+    auto big = b.allocate(16 << 20, s1);                 // bypass, 16 MiB > the cap
+    CHECK(big.ok() && big->slab_id == kBypassSlabId);
+    auto a = b.allocate(1 << 20, s1);                    // first slab (1 MiB)
+    auto c = b.allocate(1 << 20, s1);                    // second slab (2 MiB): 3 MiB in slabs
+    CHECK(a.ok() && c.ok());
+    CHECK_EQ(b.stats().bytes_reserved, std::size_t{(16 + 3) << 20});
+    auto d = b.allocate(1 << 20, s1);                    // fits the second slab
+    CHECK(d.ok());
+    auto e = b.allocate(1 << 20, s1);                    // a third slab would pass the cap
+    CHECK(!e.ok() && e.status().code() == StatusCode::kOutOfMemory);
+    for (auto* x : {&*big, &*a, &*c, &*d}) CHECK_OK(b.deallocate(*x, s1));
+    CHECK_OK(b.validate());
+  }
+  {
+    FreeListConfig cfg = fl_cfg(ReusePolicy::kCoarseStreamPoll);
+    cfg.max_total_bytes = 8 << 20;                       // two 4 MiB slabs
+    HostFreeList f(cfg);
+    const auto s1 = fake_stream(1);
+    auto big = f.allocate(32 << 20, s1);                 // bypass, 32 MiB > the cap
+    CHECK(big.ok() && big->slab_id == kBypassSlabId);
+    std::vector<Allocation> held;
+    for (int i = 0; i < 4; ++i) {                        // 4 x 2 MiB blocks: both slabs
+      auto x = f.allocate(2 << 20, s1);
+      CHECK(x.ok());
+      if (x.ok()) held.push_back(*x);
+    }
+    auto over = f.allocate(2 << 20, s1);                 // a third slab would pass the cap
+    CHECK(!over.ok() && over.status().code() == StatusCode::kOutOfMemory);
+    CHECK_OK(f.deallocate(*big, s1));
+    for (const Allocation& x : held) CHECK_OK(f.deallocate(x, s1));
+  }
+}
+
 TEST(freelist_bypass_trim_and_random_walk) {
   HostFreeList f(fl_cfg(ReusePolicy::kCoarseStreamPoll));
   const auto s1 = fake_stream(1), s2 = fake_stream(2);

@@ -20,6 +20,7 @@ poisoning and preconditions.
 """
 from __future__ import annotations
 
+import json
 import os
 import re
 import subprocess
@@ -81,3 +82,76 @@ def test_reference_graph_suite_on_gpu(gpu):
     assert MUST_RUN <= set(ran), sorted(MUST_RUN - set(ran))
     assert nfail == 0 and rc == 0, fails
     assert "(skipped: needs the host compute backend" in out
+
+
+ALLOC_BENCH = os.path.join(ROOT, "oracle", "_ref", "alloc_bench")
+
+
+@pytest.mark.gpu
+def test_reference_alloc_bench_on_gpu(gpu, tmp_path):
+    """The reference's allocator benchmark (bench/alloc_bench.cpp), built unchanged
+    against include/ and linked to this build's allocators, replays its traces
+    through RawDeviceAllocator (hipMalloc), BuddyAllocator and FreeListAllocator on
+    the GPU and completes: its own invariant checks (FATAL + abort on any failed
+    allocation or bookkeeping mismatch) all hold, and it writes its latency and
+    fragmentation CSVs."""
+    if not os.path.exists(ALLOC_BENCH):
+        if os.path.exists(REF_SRC):
+            pytest.fail(f"{ALLOC_BENCH} is missing: run `make -C oracle refsuite` (build() does)")
+        pytest.skip("the reference's allocator bench was not built (no reference tree here)")
+    print(f"running {ALLOC_BENCH} in {tmp_path}", flush=True)
+    p = subprocess.run([ALLOC_BENCH], capture_output=True, text=True, timeout=240, cwd=tmp_path)
+    out = p.stdout + p.stderr
+    print(out[-4000:])
+    assert p.returncode == 0, out[-3000:]
+    assert "FATAL" not in out
+    csvs = sorted(f.name for f in (tmp_path / "reports").iterdir())
+    assert any(c.startswith("alloc_latency_") for c in csvs), csvs
+    assert any(c.startswith("alloc_fragmentation_") for c in csvs), csvs
+    # The fragmentation tables are deterministic (a fixed-seed trace): every pool
+    # row must read what the reference published for its own allocators
+    # (tests/golden/alloc_fragmentation.json, from its RESULTS.md section 2b).
+    golden = json.load(open(os.path.join(ROOT, "tests", "golden", "alloc_fragmentation.json")))
+    tables = _fragmentation_tables(out)
+    assert list(tables) == ["uniform_pow2", "dl_transformer", "dl_transformer_bypass"], list(tables)
+    compared = 0
+    for trace, rows in tables.items():
+        for name, got in rows.items():
+            want = golden["traces"][trace][name.split("/")[0]]
+            for col in ("peak_reserved", "peak_blocks", "peak_requested", "block_eff",
+                        "reserv_eff", "utilisation", "internal_waste", "oom"):
+                assert got[col] == want[col], (trace, name, col, got[col], want[col])
+            if name != "raw":
+                assert got["largest_free_at_end"] == want["largest_free_at_end"], (trace, name)
+            compared += 1
+    assert compared == 3 * 7, compared
+
+
+def _fragmentation_tables(out: str) -> dict:
+    """The alloc bench's '2b. Fragmentation' tables, one per trace in print order:
+    {trace: {allocator: {column: "value unit"}}}."""
+    traces = re.findall(r"^--- trace: (\S+) -", out, re.M)
+    sections = out.split("=== 2b. Fragmentation")[1:]
+    assert len(sections) == len(traces), (len(sections), traces)
+    cols = ["peak_reserved", "peak_blocks", "peak_requested", "block_eff", "reserv_eff",
+            "utilisation", "internal_waste", "largest_free_at_end", "oom"]
+    tables = {}
+    for trace, sec in zip(traces, sections):
+        rows = {}
+        for line in sec.splitlines()[2:]:
+            tok = line.split()
+            if not tok or not re.match(r"^(raw|buddy|freelist)\b", tok[0]):
+                if rows:
+                    break
+                continue
+            vals, i = [], 1
+            for col in cols:
+                if col in ("block_eff", "reserv_eff", "utilisation", "oom"):
+                    vals.append(tok[i])
+                    i += 1
+                else:
+                    vals.append(f"{tok[i]} {tok[i + 1]}")
+                    i += 2
+            rows[tok[0]] = dict(zip(cols, vals))
+        tables[trace] = rows
+    return tables
