@@ -118,3 +118,31 @@ def test_reference_graph_numerics_gate(G, orc, name):
     ex.close()
     assert gate.passed, gate.detail
     assert gate.configs_compared == 9, gate.detail
+
+
+@pytest.mark.parametrize("name", GRAPHS)
+def test_plan_statistics_match_the_reference_table(G, name):
+    """Streams used, peak arena bytes and naive bytes of each reference graph under
+    the three schedules, planned as the reference's bench plans them (happens-before
+    reuse, 1 stream for sequential and 4 for the others, bench/graph_bench.cpp:333),
+    equal the reference's published table (tests/golden/graph_plan_stats.json, from
+    its RESULTS.md section 4).  Planning only: nothing is launched."""
+    import json
+    import os
+
+    golden = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                         "graph_plan_stats.json")))["graphs"][name]
+    for label, sched, streams in (("sequential", G.SchedulePolicy.kSequential, 1),
+                                  ("level_parallel", G.SchedulePolicy.kLevelParallel, 4),
+                                  ("chain_greedy", G.SchedulePolicy.kChainGreedy, 4)):
+        g, _ = G.REFERENCE_GRAPHS[name][0]()
+        ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, schedule=sched,
+                        memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=streams)
+        ex.plan()
+        info = ex.plan_info()
+        ex.close()
+        want = golden[label]
+        got = {"streams_used": info["num_streams_used"],
+               "streams_requested": info["num_streams_requested"],
+               "arena_bytes": info["arena_bytes"], "naive_bytes": info["naive_bytes"]}
+        assert got == want, (name, label, got, want)
