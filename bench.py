@@ -1267,6 +1267,48 @@ def graph_section(m, steps=5, warmup=2, gate_repeats=20, capture=True):
             + f"; numerics gate {'PASS' if gate.passed else 'FAIL'}")
     out["reference_graphs"] = ref_graphs
 
+    # The reference's transformer_block with GEMM1 -> bias+GELU fused into one node,
+    # against the unfused graph in alternating blocks (chain-greedy, 4 streams).
+    tb_spec = G.REFERENCE_GRAPHS["transformer_block"][1]
+    tb_inputs = {}
+
+    def tb_executor(build):
+        g, t = build(4096, 1024, 4096)
+        for key, (kind, seed, p0, p1) in tb_spec.items():   # shapes before the executor takes g
+            if key not in tb_inputs:
+                n_el = int(np.prod(g.shape(t[key])))
+                tb_inputs[key] = (m.fill_random(n_el, seed, p0, p1) if kind == "u"
+                                  else m.fill_normal(n_el, seed, p0, p1))
+        ex = G.Executor(g, allocator=G.AllocatorKind.kBuddy, schedule=G.SchedulePolicy.kChainGreedy,
+                        memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4)
+        ex.plan()
+        for key in tb_spec:
+            ex.set_input(t[key], tb_inputs[key])
+        return ex, t
+
+    ex_u, t_u = tb_executor(G.transformer_block)
+    ex_f, t_f = tb_executor(G.transformer_block_fused)
+    tb_u, tb_f = [], []
+    for _ in range(4):
+        tb_f.append(timed_runs(ex_f, ref_steps)[0])
+        tb_u.append(timed_runs(ex_u, ref_steps)[0])
+    y_u = ex_u.read(t_u["softmax"], 4096 * 1024)
+    y_f = ex_f.read(t_f["softmax"], 4096 * 1024)
+    ex_u.close()
+    ex_f.close()
+    tb_same = bool(np.array_equal(y_u.view(np.uint32), y_f.view(np.uint32)))
+    out["transformer_block_fused"] = {
+        "shape": "transformer_block(4096, 1024, 4096), chain_greedy, 4 streams",
+        "unfused_wall_ms": round(float(np.median(tb_u)), 4),
+        "fused_wall_ms": round(float(np.median(tb_f)), 4),
+        "speedup": round(float(np.median(tb_u)) / float(np.median(tb_f)), 4),
+        "blocks": f"4 alternating blocks of {ref_steps} runs each; medians",
+        "parity": {"ok": tb_same, "same_output_bits_as_unfused": tb_same},
+    }
+    log(f"transformer_block fused: {out['transformer_block_fused']['fused_wall_ms']} ms against "
+        f"{out['transformer_block_fused']['unfused_wall_ms']} ms unfused "
+        f"({out['transformer_block_fused']['speedup']}x), same bits: {tb_same}")
+
     # The HIP-graph capture part (skipped with capture=False: under rocprofv3's kernel
     # trace the host process crashed inside it, so profiling runs leave it out).
     if capture:
@@ -1621,6 +1663,9 @@ def headline(detail: dict, detail_file: str | None) -> dict:
         if fused:
             extra["graph_mlp"].update(fused_wall_ms=fused.get("wall_ms"),
                                       fused_tflops=fused.get("tflops"))
+        tb = graph.get("transformer_block_fused")
+        if tb:
+            extra["graph_mlp"]["transformer_block_fused_speedup"] = tb.get("speedup")
     if graph.get("gates_passed") is not None:
         extra["graph_gates_passed"] = graph["gates_passed"]
     if graph.get("capture_choice"):

@@ -489,6 +489,23 @@ def transformer_block(tokens: int, d_model: int, d_ff: int):
                "softmax": y, "outs": [y]}
 
 
+def transformer_block_fused(tokens: int, d_model: int, d_ff: int):
+    """transformer_block with its GEMM -> bias+GELU pair as one GemmBiasAct node
+    (the bias and GELU in GEMM1's epilogue): three nodes, the same tensors under
+    the same names except "gemm1" (never stored), and the same output bits."""
+    g = Graph()
+    x = g.add_input((tokens, d_model), "x")
+    w1 = g.add_input((d_model, d_ff), "W1")
+    b1 = g.add_input((d_ff,), "b1")
+    w2 = g.add_input((d_ff, d_model), "W2")
+    h = g.add_gemm_bias_act(x, w1, b1, "gemm1_bias_gelu", act=3)
+    g2 = g.add_gemm(h, w2, "gemm2")
+    y = g.add_softmax(g2, "softmax")
+    g.mark_output(y)
+    return g, {"x": x, "W1": w1, "b1": b1, "W2": w2, "bias_gelu": h, "gemm2": g2,
+               "softmax": y, "outs": [y]}
+
+
 # name -> (builder, {input name: ("u", seed, lo, hi) | ("n", seed, mean, sigma)}): the
 # five graphs the reference's graph bench runs, at its shapes (graph_bench.cpp:477-481),
 # with seeded inputs drawn by fill_random (U[lo, hi)) or fill_normal (N(mean, sigma^2)).

@@ -146,3 +146,37 @@ def test_plan_statistics_match_the_reference_table(G, name):
                "streams_requested": info["num_streams_requested"],
                "arena_bytes": info["arena_bytes"], "naive_bytes": info["naive_bytes"]}
         assert got == want, (name, label, got, want)
+
+
+def test_fused_transformer_block_has_the_unfused_bits(G, orc):
+    """transformer_block_fused (GEMM1 + bias + GELU in one node) against the
+    reference's transformer_block at a reduced shape: the same H and output bits on
+    a per-tensor plan and on a 4-stream plan with reuse over poisoned buffers."""
+    T, D, F = 512, 256, 1024
+    inp = {"x": orc.fill_normal(T * D, 0x4500, 0.0, 1.0),
+           "W1": orc.fill_normal(D * F, 0x4501, 0.0, 0.02),
+           "b1": orc.fill_normal(F, 0x4502, 0.0, 0.01),
+           "W2": orc.fill_normal(F * D, 0x4503, 0.0, 0.02)}
+
+    def run(build, **kw):
+        g, t = build(T, D, F)
+        ex = G.Executor(g, **kw)
+        ex.plan()
+        for k, v in inp.items():
+            ex.set_input(t[k], v)
+        ex.run_sync()
+        ex.run_sync()
+        got = {k: ex.read(t[k], n) for k, n in (("bias_gelu", T * F), ("softmax", T * D))
+               if kw.get("memory") == G.MemoryPolicy.kAllocPerTensor or k == "softmax"}
+        ex.close()
+        return got
+
+    per = dict(schedule=G.SchedulePolicy.kSequential, memory=G.MemoryPolicy.kAllocPerTensor,
+               num_streams=1)
+    gold = run(G.transformer_block, **per)
+    fused = run(G.transformer_block_fused, **per)
+    for k in ("bias_gelu", "softmax"):
+        assert np.array_equal(gold[k].view(np.uint32), fused[k].view(np.uint32)), k
+    reuse = run(G.transformer_block_fused, schedule=G.SchedulePolicy.kChainGreedy,
+                memory=G.MemoryPolicy.kReuseHappensBefore, num_streams=4, poison_buffers=True)
+    assert np.array_equal(gold["softmax"].view(np.uint32), reuse["softmax"].view(np.uint32))
