@@ -423,12 +423,13 @@ int launch_rocblas(const float* a, const float* b, float* c, int m, int n, int k
 // staged one; `fused` picks the instantiations with the bias + activation
 // epilogue, which route shapes exactly as the plain ones do (so a fused launch
 // accumulates in the plain launch's order).
-int launch_mfma(const Spec& sp, bool fused, const float* a, const float* b, float* c, int64_t m,
-                int64_t n, int64_t k, float alpha, float beta, EpiArgs epi, hipStream_t s) {
+int launch_mfma(const char* who, const Spec& sp, bool fused, const float* a, const float* b,
+                float* c, int64_t m, int64_t n, int64_t k, float alpha, float beta, EpiArgs epi,
+                hipStream_t s) {
   const int64_t tiles_m = (m + sp.tile_m - 1) / sp.tile_m;
   const int64_t tiles_n = (n + sp.tile_n - 1) / sp.tile_n;
   if (tiles_m * tiles_n > 2147483647LL)
-    return invalid("launch_gemm_f32: too many tiles for one launch");
+    return invalid(std::string(who) + ": too many tiles for one launch");
   const bool whole = sp.mfma_even && m % sp.tile_m == 0 && n % sp.tile_n == 0 &&
                      k % sp.tile_k == 0 &&
                      (!sp.even_dma || (static_cast<int64_t>(sp.tile_m) * k < (int64_t{1} << 30) &&
@@ -436,7 +437,7 @@ int launch_mfma(const Spec& sp, bool fused, const float* a, const float* b, floa
   MfmaFn fn = whole ? (fused ? sp.mfma_even_f : sp.mfma_even) : (fused ? sp.mfma_f : sp.mfma);
   const dim3 block = whole ? dim3(static_cast<unsigned>(sp.even_threads), 1, 1) : sp.block;
   if (tiles_m * tiles_n * static_cast<int64_t>(block.x) > int64_t{UINT32_MAX})
-    return invalid("launch_gemm_f32: tiles x lanes exceed the grid's 32-bit work size; use a "
+    return invalid(std::string(who) + ": tiles x lanes exceed the grid's 32-bit work size; use a "
                    "larger tile");
   fn<<<static_cast<unsigned>(tiles_m * tiles_n), block, 0, s>>>(
       a, b, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), alpha, beta,
@@ -475,7 +476,9 @@ int mcke_launch_gemm_f32(const float* a, const float* b, float* c, int64_t m, in
   Spec sp;
   if (int rc = gemm_spec(variant, tile, vec4, sp)) return rc;
 
-  if (sp.mfma) return launch_mfma(sp, false, a, b, c, m, n, k, alpha, beta, EpiArgs{nullptr, 0}, s);
+  if (sp.mfma)
+    return launch_mfma("launch_gemm_f32", sp, false, a, b, c, m, n, k, alpha, beta,
+                       EpiArgs{nullptr, 0}, s);
 
   // grid.x walks C column tiles and grid.y C row tiles for every ladder kernel
   // (kNaiveUncoalesced only changes which lane index runs along a row).
@@ -507,8 +510,8 @@ int mcke_launch_gemm_bias_act_f32(const float* a, const float* b, const float* b
                     aligned(y, 16);
   Spec sp;
   if (int rc = gemm_spec(MCKE_GEMM_MFMA_F32, tile, vec4, sp)) return rc;
-  return launch_mfma(sp, true, a, b, y, m, n, k, alpha, 0.0f, EpiArgs{bias, activation},
-                     static_cast<hipStream_t>(stream));
+  return launch_mfma("launch_gemm_bias_act_f32", sp, true, a, b, y, m, n, k, alpha, 0.0f,
+                     EpiArgs{bias, activation}, static_cast<hipStream_t>(stream));
 }
 
 int mcke_gemm_kernel_attrs(int variant, const mcke_gemm_tile* tile, mcke_kernel_attrs* out) {
