@@ -587,3 +587,30 @@ def test_capture_if_faster_keeps_the_faster_path(G, orc, plan):
         for got, want in zip(run(ex), gold):
             assert np.array_equal(got, want), f"{plan} run {rep} (captured={d['captured']})"
     ex.close()
+
+
+def test_captured_fused_mlp_replays_match_unfused_eager(G, orc):
+    """The fused MLP (GemmBiasAct nodes) captured into one HIP graph: every replay,
+    with unrelated eager work between them, gives the unfused graph's eager bits."""
+    import mcke_amd as m
+    T, D, F = 256, 128, 512
+    kw = dict(schedule=G.SchedulePolicy.kChainGreedy, memory=G.MemoryPolicy.kReuseHappensBefore,
+              num_streams=4, poison_buffers=True)
+    inp = _mlp_inputs(orc, T, D, F)
+    gold = _eager_y(G, inp, T, D, F, **kw)
+    g, t = G.mlp_block_fused(T, D, F)
+    ex = G.Executor(g, **kw)
+    ex.plan()
+    for k, v in inp.items():
+        ex.set_input(t[k], v)
+    ex.capture()
+    assert ex.captured
+    scratch_x = m.DeviceBuffer.from_array(orc.fill_normal(4096, 9))
+    scratch_y = m.DeviceBuffer(4096 * 4)
+    for rep in range(4):
+        ex.run_sync()
+        got = ex.read(t["y"], T * D)
+        assert np.array_equal(got.view(np.uint32), gold.view(np.uint32)), f"replay {rep}"
+        m.launch_activation_f32(scratch_x, scratch_y, 4096, m.Activation.kGeluTanh, 4).throw_if_error()
+        m.device_synchronize()
+    ex.close()
